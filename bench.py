@@ -1,0 +1,283 @@
+"""Benchmark of the MI355X projection path (one GPU).
+
+Default run (the driver's contract): the BASELINE configs[1] workload — the fused gate-up projection with the
+SiLU.mul epilogue, x [288, 5120] bf16 ~ N(0,1), W_gu [2 x 17408, 5120] ~ N(0, 0.02^2), out [288, 17408] bf16 —
+as W untimed warm-up steps and then exactly K timed steps, captured in one HIP graph and replayed once between
+two synchronizations. A step is one call of the fused projection over the batch; the weights rotate over two
+copies (712 MB), more than the 256 MB Infinity Cache, so every step streams its weights from HBM.
+
+Prints ONE JSON line with the metric, the roofline of the dominant kernel (HIP events on the launch stream), the
+CPU baseline (the oracle's torch CPU path on a bounded sample of the same workload, on this host's cores) and the
+per-shape table at M = 7 / 288 / 539 for the five projection shapes.
+
+Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
+the 64-layer projection stack at M = 539 in one graph replay).
+"""
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "bf16 proj GEMM TFLOP/s + HBM GB/s, % roofline, at M=7/288/539 on 1 MI355X"
+
+
+def load():
+    import __graft_entry__
+    pkg = __graft_entry__.load_package()
+    from importlib import import_module
+    return pkg, import_module("open_jev_fast_amd.ext"), import_module("open_jev_fast_amd.perf")
+
+
+def make_weights(N, K, copies, std=0.02, seed=0, dev="cuda"):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    return [(torch.randn(N, K, generator=g, device=dev) * std).bfloat16() for _ in range(copies)]
+
+
+def shape_call(ext, kind, x, w, res=None, w1=None):
+    if kind == "plain":
+        return lambda: ext.mm(x, w)
+    if kind == "silu":
+        return lambda: ext.mm_silu_mul(x, w)
+    return lambda: ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6)
+
+
+def measure_shape(ext, perf, name, M, iters=20, reps=5):
+    N, K, kind = perf.SHAPES[name]
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(M)
+    x = torch.randn(M, K, generator=g, device=dev).bfloat16()
+    ws = make_weights(N, K, perf.copies_for(N * K * 2), seed=M + 1)
+    res = torch.randn(M, N, generator=g, device=dev).bfloat16() if kind == "residual" else None
+    w1 = torch.ones(N, device=dev) if kind == "residual" else None
+    fns = [shape_call(ext, kind, x, w, res, w1) for w in ws]
+    t = perf.gpu_time(fns, iters=iters, reps=reps)
+    r = perf.roofline(M, N, K, kind, t)
+    del ws
+    return r
+
+
+def cpu_baseline(M, I, K, budget_s=15.0):
+    """The oracle's CPU path (BASELINE.md plan: torch.matmul on bf16 CPU tensors + the same SiLU.mul epilogue) on
+    a row slice of W_gu sized to about `budget_s` seconds; median of 5 after 2 warm-ups."""
+    from oracle import proj_oracle as O
+    torch.set_num_threads(os.cpu_count() or 1)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g).bfloat16()
+
+    def run(rows):
+        wg = (torch.randn(rows, K, generator=g) * 0.02).bfloat16()
+        wu = (torch.randn(rows, K, generator=g) * 0.02).bfloat16()
+        w = torch.cat([wg, wu], 0)
+        fn = lambda: O.silu_mul(torch.matmul(x, w.t()))   # noqa: E731
+        return fn
+
+    probe_rows = 512
+    fn = run(probe_rows)
+    fn()
+    t0 = time.perf_counter()
+    fn()
+    t_probe = time.perf_counter() - t0
+    rows = int(min(I, max(probe_rows, probe_rows * (budget_s / 7.0) / max(t_probe, 1e-6))))
+    rows -= rows % 8
+    fn = run(rows)
+    for _ in range(2):
+        fn()
+    ts = []
+    for _ in range(5):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    t = statistics.median(ts)
+    flops = 2.0 * M * (2 * rows) * K
+    return {"value": round(flops / t / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"gate-up+SiLU.mul M={M} K={K}, {rows} of {I} gate/up row pairs "
+                      f"({2 * rows} of {2 * I} W_gu rows), torch CPU bf16 matmul, median of 5 after 2 warm-ups "
+                      f"({t * 1e3:.1f} ms per call; os.cpu_count()={os.cpu_count()})"}
+
+
+def main_default(args, pkg, ext, perf):
+    M, I, K = 288, 17408, 5120
+    N = 2 * I
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(M, K, generator=g, device=dev).bfloat16()
+    ws = make_weights(N, K, 2, seed=2)
+    plan = pkg._lib.plan(M, N, K, pkg._lib.KIND_SILU_MUL)
+    fns = [lambda w=w: ext.mm_silu_mul(x, w) for w in ws]
+
+    # warm-up (untimed), then one graph of exactly K steps
+    for i in range(args.warmup):
+        fns[i % 2]()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            for i in range(args.steps):
+                fns[i % 2]()
+    torch.cuda.synchronize()
+    graph.replay()  # upload / first replay (untimed)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cur = torch.cuda.current_stream()
+    torch.cuda.synchronize()
+    a.record(cur)
+    graph.replay()
+    b.record(cur)
+    torch.cuda.synchronize()
+    ms = a.elapsed_time(b) / args.steps
+    r = perf.roofline(M, N, K, "silu", ms * 1e-3)
+    flops, nbytes = perf.work(M, N, K, "silu")
+
+    # per-launch duration of the dominant kernel, HIP events on the stream the kernel runs on (eager launches)
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_k = 50
+    ev0.record(cur)
+    for i in range(n_k):
+        fns[i % 2]()
+    ev1.record(cur)
+    torch.cuda.synchronize()
+    k_s = ev0.elapsed_time(ev1) * 1e-3 / n_k
+    bound = r["bound"]
+    if bound == "hbm":
+        achieved, peak, unit = nbytes / k_s / 1e9, perf.HBM_PEAK / 1e9, "GB/s"
+    else:
+        achieved, peak, unit = flops / k_s / 1e12, perf.MFMA_BF16_PEAK / 1e12, "TFLOP/s"
+    roof = {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles("gate_up_silu_M288"),
+            "kernel_us": round(k_s * 1e6, 2), "roofline_frac_of_min_bound": round(r["roof_us"] / (k_s * 1e6), 4)}
+    del ws, fns, graph
+
+    shapes = {}
+    if not args.no_shapes:
+        for name in perf.SHAPES:
+            for m in (7, 288, 539):
+                rr = measure_shape(ext, perf, name, m)
+                shapes[f"{name}_M{m}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}
+    cpu = None if args.no_cpu else cpu_baseline(M, I, K)
+    line = {
+        "metric": METRIC, "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic: seeded x ~ N(0,1), W ~ N(0,0.02^2), bf16; 2 rotating weight copies",
+        "config": {"workload": "gate_up_silu: BASELINE configs[1], fused gate-up + SiLU.mul, M=288 K=5120 "
+                               "I=17408 (W_gu 34816x5120)", "M": M, "N": N, "K": K,
+                   "plan": {"tile": plan.tile, "splitk": plan.splitk, **pkg._lib.tile_info(plan.tile)}},
+        "gbs": round(r["gbs"], 1), "roofline_frac": round(r["frac"], 4),
+        "roofline": roof, "cpu_baseline": cpu, "shapes": shapes,
+    }
+    print(json.dumps(line), flush=True)
+
+
+def traffic_from_profiles(key):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the copy-kernel
+    calibration), recorded in profiles/traffic.json; None when not measured."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(key)
+    except (OSError, ValueError):
+        return None
+
+
+def main_sweep(args, pkg, ext, perf):
+    Ms = [int(m) for m in args.m.split(",")] if args.m else perf.M_SWEEP
+    names = args.shapes.split(",") if args.shapes else list(perf.SHAPES)
+    for name in names:
+        for m in Ms:
+            rr = measure_shape(ext, perf, name, m)
+            N, K, kind = perf.SHAPES[name]
+            c = pkg._lib.plan(m, N, K, {"plain": 0, "silu": 1, "residual": 2}[kind])
+            print(json.dumps({"shape": name, "M": m, "N": N, "K": K, "tile": c.tile, "splitk": c.splitk,
+                              **{k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}}), flush=True)
+
+
+def main_stack(args, pkg, ext, perf):
+    """48 linear-attention + 16 full-attention layers, hidden 5120, MLP 17408, M = 539.
+    Each layer: in-proj, out-proj + residual + RMSNorm, gate-up + SiLU.mul, down + residual + RMSNorm, back to
+    back in one graph. The attention cores between in-proj and out-proj are out of scope: the out-proj reads a
+    fixed activation of the right shape."""
+    M, H, I = 539, 5120, 17408
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(5)
+    std = 0.02
+    lin_in, full_in, lin_out_k, full_out_k = 16384, 14336, 6144, 6144
+    layers = []
+    for i in range(64):
+        full = (i % 4) == 3
+        n_in = full_in if full else lin_in
+        layers.append(dict(
+            w_in=(torch.randn(n_in, H, generator=g, device=dev) * std).bfloat16(),
+            w_out=(torch.randn(H, full_out_k if full else lin_out_k, generator=g, device=dev) * std).bfloat16(),
+            w_gu=(torch.randn(2 * I, H, generator=g, device=dev) * std).bfloat16(),
+            w_dn=(torch.randn(H, I, generator=g, device=dev) * std).bfloat16()))
+    h0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    hn0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    y_att = torch.randn(M, lin_out_k, generator=g, device=dev).bfloat16()
+    w1 = torch.ones(H, device=dev)
+
+    def forward():
+        h, hn = h0, hn0
+        for d in layers:
+            ext.mm(hn, d["w_in"])
+            h, hn = ext.mm_residual_rmsnorm(h, y_att, d["w_out"], w1, None, 1e-6)
+            m = ext.mm_silu_mul(hn, d["w_gu"])
+            h, hn = ext.mm_residual_rmsnorm(h, m, d["w_dn"], w1, None, 1e-6)
+        return h, hn
+
+    t = perf.gpu_time([forward], iters=1, reps=args.steps, warmup=2)
+    flops = nbytes = 0.0
+    for i in range(64):
+        full = (i % 4) == 3
+        for (N, K, kind) in (((full_in if full else lin_in), H, "plain"), (H, lin_out_k, "residual"),
+                             (2 * I, H, "silu"), (H, I, "residual")):
+            f, b = perf.work(M, N, K, kind)
+            flops += f
+            nbytes += b
+    t_roof = max(nbytes / perf.HBM_PEAK, flops / perf.MFMA_BF16_PEAK)
+    print(json.dumps({"stack": "64-layer projection stack (48 lin + 16 full)", "M": M, "ms": round(t * 1e3, 3),
+                      "tflops": round(flops / t / 1e12, 1), "gbs": round(nbytes / t / 1e9, 1),
+                      "roof_ms": round(t_roof * 1e3, 3), "frac": round(t_roof / t, 4),
+                      "bound": "hbm" if nbytes / perf.HBM_PEAK >= flops / perf.MFMA_BF16_PEAK else "mfma"}),
+          flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--sweep", action="store_true")
+    ap.add_argument("--stack", action="store_true")
+    ap.add_argument("--m", default="")
+    ap.add_argument("--shapes", default="")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-shapes", action="store_true")
+    args = ap.parse_args()
+    ws = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or ws != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path (the projections would shard as "
+              "column/row tensor parallelism; see the design notes). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    pkg, ext, perf = load()
+    if args.sweep:
+        main_sweep(args, pkg, ext, perf)
+    elif args.stack:
+        main_stack(args, pkg, ext, perf)
+    else:
+        main_default(args, pkg, ext, perf)
+
+
+if __name__ == "__main__":
+    main()

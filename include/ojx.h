@@ -1,0 +1,124 @@
+/*
+ * ojx — MI355X (gfx950) dense bf16 projection kernels for the open-jev-fast 27B hybrid forward.
+ *
+ * C-ABI of libojx.so: plain C, raw device pointers, element counts and a HIP stream handle; no torch types.
+ * All bf16 tensors are raw 16-bit patterns, row-major. A projection computes
+ *     y[M,N] = x[M,K] . W[N,K]^T      (bf16 inputs, fp32 accumulation, bf16 output)
+ * with both x and W K-contiguous, the layout of the reference's lt_matmul (src/lt.cpp:22-29) and F.linear.
+ *
+ * Every entry point returns OJX_OK (0) or an error code; ojx_last_error() gives the message of the last failure
+ * on the calling thread. Launches go on the given stream, never synchronize and never allocate, so they can be
+ * captured into a HIP graph. Entry points that take a workspace need ojx_workspace_bytes() bytes of device memory
+ * there (0 bytes when the plan has no split-K).
+ *
+ * Global state (the plan table, kernel attributes) is read-only after the first call; concurrent calls on
+ * different streams are safe as long as they do not share output or workspace buffers.
+ */
+#ifndef OJX_H
+#define OJX_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* ojx_stream_t; /* hipStream_t; NULL = the null stream */
+
+enum {
+  OJX_OK = 0,
+  OJX_ERR_ARG = 1,       /* null / misaligned pointer, bad stride */
+  OJX_ERR_SHAPE = 2,     /* unsupported shape (e.g. N or K not a multiple of 8, H/8 > 1024) */
+  OJX_ERR_WORKSPACE = 3, /* workspace missing or too small for the plan */
+  OJX_ERR_CONFIG = 4,    /* tile id / split-K count out of range */
+  OJX_ERR_HIP = 5        /* a HIP runtime call failed */
+};
+
+enum {
+  OJX_KIND_PLAIN = 0,     /* y = x W^T */
+  OJX_KIND_SILU_MUL = 1,  /* gate-up projection with the SiLU(gate) * up epilogue */
+  OJX_KIND_RESIDUAL = 2   /* out / o_proj / down projection with residual add (+ RMSNorm) */
+};
+
+/* One kernel configuration: a tile shape from the tile registry and a split-K count. */
+typedef struct {
+  int32_t tile;
+  int32_t splitk;
+} ojx_cfg;
+
+const char* ojx_last_error(void);
+const char* ojx_version(void);
+
+/* Sets kernel attributes on the current device. Optional: every launch does it on first use. */
+int ojx_init(void);
+
+/* Tile registry: info6 = {BN (W rows), BM (x rows), BK, waves along N, waves along M, threads}. */
+int ojx_num_tiles(void);
+int ojx_tile_info(int32_t tile, int32_t* info6);
+
+/* Plan lookup for a shape: a static table measured offline on MI355X, with a heuristic for shapes not in it.
+ * Never times anything, so it is safe during graph capture.
+ * Replaces the per-shape cuBLASLt heuristic/search: lt_setup (src/lt.cpp:15-42), _tune (src/fastmodel.py:114-132),
+ * lt2_plan / lt2_search (src/lt.cpp:64-159). For OJX_KIND_SILU_MUL, N is the packed 2*I. */
+int ojx_plan(int64_t M, int64_t N, int64_t K, int32_t kind, ojx_cfg* out);
+
+/* Candidate configurations for a shape (every tile x split-K that is valid), the list a tuner sweeps.
+ * Mirrors lt_setup's algorithm count and lt_matmul's algorithm index (src/lt.cpp:15-55). */
+int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind);
+int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, ojx_cfg* out);
+
+/* Workspace bytes the call needs with cfg (NULL = the plan's choice). */
+int64_t ojx_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg);
+
+/* y[M,N] (row stride ldy) = x[M,K] (row stride ldx) . W[N,K]^T (row stride ldw).
+ * Replaces lt_matmul (src/lt.cpp:43-55) / F.linear as called by _mm (src/fastmodel.py:168-175).
+ * N, K, ldx, ldw multiples of 8; ldy a multiple of 4. cfg NULL = the plan's choice. */
+int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                  int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                  ojx_stream_t stream);
+
+/* Split-K partial products in fp32: parts[s][M][N] = x[:, K_s] . W[:, K_s]^T over S contiguous K ranges.
+ * Replaces _skmm's torch.bmm(x.view(M,S,K/S).transpose(0,1), Wsk, out_dtype=fp32) (src/fastmodel.py:158-166)
+ * and lt2_run (src/lt.cpp:160-169); W stays [N,K] (no [S,K/S,N] copy). Split s covers K range
+ * [s*c, min(K,(s+1)*c)) with c = K/S rounded up to a multiple of 8, i.e. the reference's K/S chunks whenever
+ * K is a multiple of 8*S. tile < 0 = the plan's tile. */
+int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                        int64_t ldw, int32_t S, int32_t tile, ojx_stream_t stream);
+
+/* out[M,I] = bf16(bf16(silu(g)) * u) with [g | u] = x . W_gu^T, W_gu packed by ojx_pack_gate_up ([2I, K]).
+ * Replaces _silu_mul(_mm(hn, w_gu)) (src/fastmodel.py:478,190-194; src/kernels.cu:1304-1331) in one pass. */
+int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t M, int64_t I, int64_t K,
+                      void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream);
+
+/* h_out = bf16(residual + bf16(x . W^T)); if hn_out != NULL also
+ * hn_out = bf16((h * rsqrt(mean(h^2) + eps)) * w1), zero on rows where rowmask == 0 (rowmask may be NULL).
+ * Replaces _res (src/fastmodel.py:196-203): split-K GEMM + add_rmsnorm_sk2 (src/kernels.cu:1444-1501) or
+ * GEMM + add_rmsnorm (src/kernels.cu:41-73). h_out may alias residual. RMSNorm needs N % 8 == 0, N/8 <= 1024. */
+int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual, const float* w1,
+                              const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
+                              int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                              ojx_stream_t stream);
+
+/* Standalone epilogues, same arguments and semantics as the reference extension's functions. */
+/* add_rmsnorm (src/kernels.cu:41-73, 755-767): delta may be NULL (then h_out is not written: h == x). */
+int ojx_add_rmsnorm(const void* x, const void* delta, const float* w1, const int32_t* rowmask, float eps,
+                    void* h_out, void* hn_out, int64_t M, int64_t H, ojx_stream_t stream);
+/* add_rmsnorm_sk / add_rmsnorm_sk2 (src/kernels.cu:475-515, 1444-1501): parts fp32 [S, M, H]. */
+int ojx_add_rmsnorm_sk(const void* x, const float* parts, int32_t S, const float* w1, const int32_t* rowmask,
+                       float eps, void* h_out, void* hn_out, int64_t M, int64_t H, ojx_stream_t stream);
+/* silu_mul (src/kernels.cu:76-89, 769-777): gu [M, 2I] = [gate | up] -> out [M, I]. */
+int ojx_silu_mul(const void* gu, void* out, int64_t M, int64_t I, ojx_stream_t stream);
+/* silu_mul_lut (src/kernels.cu:1304-1331): tab = the 65536-entry bf16 silu table from ojx_act_tables. */
+int ojx_silu_mul_lut(const void* gu, const void* tab, void* out, int64_t M, int64_t I, ojx_stream_t stream);
+/* act_tables (src/kernels.cu:1288-1301): silu_b bf16[65536], sig_f fp32[65536]. */
+int ojx_act_tables(void* silu_b, float* sig_f, ojx_stream_t stream);
+
+/* Weight layout for the fused gate-up: packed[2I, K], rows in blocks of 8 = gate rows 4b..4b+3, up rows 4b..4b+3.
+ * Replaces the load-time torch.cat([gate, up]) of src/fastmodel.py:90. I must be a multiple of 4, K of 8. */
+int ojx_pack_gate_up(const void* gate, const void* up, void* packed, int64_t I, int64_t K, ojx_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OJX_H */

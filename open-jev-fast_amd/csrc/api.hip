@@ -1,0 +1,373 @@
+// C-ABI of libojx.so (declared in include/ojx.h): argument checks, plan lookup, and the launch sequences of the
+// fused projection entry points.
+#include "ojx_internal.h"
+#include "ojx.h"
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_err = buf;
+  return code;
+}
+
+int hip_check(hipError_t e, const char* what) {
+  if (e == hipSuccess) return OJX_OK;
+  return fail(OJX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+inline int64_t kchunk_for(int64_t K, int64_t S) { return cdiv(cdiv(K, S), 8) * 8; }
+
+struct PlanEntry {
+  int64_t M, N, K;
+  int32_t kind, tile, splitk;
+};
+
+// Measured on MI355X by the offline sweep (tuning script in the package); shapes not listed use heuristic_plan.
+const PlanEntry kPlan[] = {
+#include "plan_table.inc"
+};
+
+constexpr int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
+constexpr int kMaxSplit = 16;
+
+bool cfg_fits(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
+  (void)M; (void)N;
+  if (c.tile < 0 || c.tile >= ojx::num_tiles()) return false;
+  if (c.splitk < 1 || c.splitk > kMaxSplit) return false;
+  const int64_t ch = kchunk_for(K, c.splitk);
+  return (c.splitk - 1) * ch < K;  // every split owns a non-empty K range
+}
+
+ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
+  (void)kind;
+  ojx_cfg c;
+  if (M <= 16) c.tile = 0;
+  else if (M <= 32) c.tile = 2;
+  else if (M <= 64) c.tile = 4;
+  else if (M <= 128) c.tile = 6;
+  else if (M <= 384) c.tile = 10;
+  else c.tile = 7;
+  const ojx::TileInfo* t = ojx::tile_info(c.tile);
+  const int64_t tiles = cdiv(N, t->bn) * cdiv(M, t->bm);
+  int64_t S = 1;
+  while (S < 8 && tiles * S * 2 <= 512 && K / (S * 2) >= 512) S *= 2;
+  c.splitk = (int32_t)S;
+  return c;
+}
+
+int resolve(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg, ojx_cfg* out) {
+  if (cfg != nullptr) {
+    if (!cfg_fits(M, N, K, *cfg))
+      return fail(OJX_ERR_CONFIG, "config (tile %d, splitk %d) invalid for M=%lld N=%lld K=%lld", cfg->tile,
+                  cfg->splitk, (long long)M, (long long)N, (long long)K);
+    *out = *cfg;
+    return OJX_OK;
+  }
+  return ojx_plan(M, N, K, kind, out);
+}
+
+int check_dims(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N <= 0 || K <= 0) return fail(OJX_ERR_SHAPE, "bad shape M=%lld N=%lld K=%lld", (long long)M,
+                                              (long long)N, (long long)K);
+  if (M >= (1LL << 31) || N >= (1LL << 31) || K >= (1LL << 31))
+    return fail(OJX_ERR_SHAPE, "shape dimension exceeds 2^31");
+  if (N % 8 != 0 || K % 8 != 0)
+    return fail(OJX_ERR_SHAPE, "N (%lld) and K (%lld) must be multiples of 8", (long long)N, (long long)K);
+  return OJX_OK;
+}
+
+// One GEMM launch with the given tile / split count and epilogue.
+int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
+         const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+  const ojx::TileInfo* t = ojx::tile_info(c.tile);
+  ojx::GemmParams p;
+  p.W = static_cast<const uint16_t*>(w);
+  p.ldw = ldw;
+  p.X = static_cast<const uint16_t*>(x);
+  p.ldx = ldx;
+  p.out = out;
+  p.ldo = ldo;
+  p.res = static_cast<const uint16_t*>(res);
+  p.ldr = ldr;
+  p.part_stride = M * N;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.kchunk = (int)kchunk_for(K, c.splitk);
+  p.tiles_n = (int)cdiv(N, t->bn);
+  p.tiles_m = (int)cdiv(M, t->bm);
+  p.splits = c.splitk;
+  if ((int64_t)p.tiles_n * p.tiles_m * p.splits >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "grid too large");
+  return hip_check(ojx::launch_gemm(c.tile, epi, p, st), "gemm launch");
+}
+
+int check_operands(const void* x, const void* w, int64_t ldx, int64_t ldw, int64_t K) {
+  if (x == nullptr || w == nullptr) return fail(OJX_ERR_ARG, "null x or w");
+  if (!aligned(x, 16) || !aligned(w, 16)) return fail(OJX_ERR_ARG, "x and w must be 16-byte aligned");
+  if (ldx < K || ldw < K || ldx % 8 != 0 || ldw % 8 != 0)
+    return fail(OJX_ERR_ARG, "row strides ldx=%lld ldw=%lld must be >= K and multiples of 8", (long long)ldx,
+                (long long)ldw);
+  return OJX_OK;
+}
+
+int check_ws(void* ws, int64_t ws_bytes, int64_t need) {
+  if (need == 0) return OJX_OK;
+  if (ws == nullptr || ws_bytes < need)
+    return fail(OJX_ERR_WORKSPACE, "workspace of %lld bytes needed, %lld given", (long long)need,
+                (long long)(ws == nullptr ? 0 : ws_bytes));
+  if (!aligned(ws, 16)) return fail(OJX_ERR_ARG, "workspace must be 16-byte aligned");
+  return OJX_OK;
+}
+
+int check_rows(int64_t M, int64_t H) {
+  if (M < 0 || H <= 0 || H % 8 != 0 || H / 8 > 1024)
+    return fail(OJX_ERR_SHAPE, "row kernels need H %% 8 == 0 and H/8 <= 1024 (H=%lld)", (long long)H);
+  if (M >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "M exceeds 2^31");
+  return OJX_OK;
+}
+
+#define OJX_TRY(expr)               \
+  do {                              \
+    const int rc_ = (expr);         \
+    if (rc_ != OJX_OK) return rc_;  \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+const char* ojx_last_error(void) { return g_err.c_str(); }
+const char* ojx_version(void) { return "ojx 0.1 gfx950"; }
+
+int ojx_init(void) { return hip_check(ojx::init_tiles(), "kernel attribute setup"); }
+
+int ojx_num_tiles(void) { return ojx::num_tiles(); }
+
+int ojx_tile_info(int32_t tile, int32_t* info6) {
+  const ojx::TileInfo* t = ojx::tile_info(tile);
+  if (t == nullptr) return fail(OJX_ERR_CONFIG, "tile %d out of range [0, %d)", tile, ojx::num_tiles());
+  if (info6 == nullptr) return fail(OJX_ERR_ARG, "null info");
+  info6[0] = t->bn; info6[1] = t->bm; info6[2] = t->bk; info6[3] = t->wn; info6[4] = t->wm; info6[5] = t->threads;
+  return OJX_OK;
+}
+
+int ojx_plan(int64_t M, int64_t N, int64_t K, int32_t kind, ojx_cfg* out) {
+  if (out == nullptr) return fail(OJX_ERR_ARG, "null plan output");
+  if (kind < OJX_KIND_PLAIN || kind > OJX_KIND_RESIDUAL) return fail(OJX_ERR_ARG, "unknown kind %d", kind);
+  for (const PlanEntry& e : kPlan) {
+    if (e.M == M && e.N == N && e.K == K && e.kind == kind) {
+      ojx_cfg c{e.tile, e.splitk};
+      if (cfg_fits(M, N, K, c)) { *out = c; return OJX_OK; }
+    }
+  }
+  *out = heuristic_plan(M, N, K, kind);
+  if (!cfg_fits(M, N, K, *out)) *out = ojx_cfg{out->tile, 1};
+  return OJX_OK;
+}
+
+static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
+  if (!cfg_fits(M, N, K, c)) return false;
+  const ojx::TileInfo* t = ojx::tile_info(c.tile);
+  const int64_t mp = cdiv(M > 0 ? M : 1, 16) * 16;
+  if (t->bm >= 2 * mp) return false;                   // more than half the x tile would be padding
+  if (c.splitk > 1 && kchunk_for(K, c.splitk) < 256) return false;
+  return true;
+}
+
+int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind) {
+  (void)kind;
+  int n = 0;
+  for (int t = 0; t < ojx::num_tiles(); ++t)
+    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s}) ? 1 : 0;
+  return n;
+}
+
+int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, ojx_cfg* out) {
+  (void)kind;
+  if (out == nullptr) return fail(OJX_ERR_ARG, "null candidate output");
+  int n = 0;
+  for (int t = 0; t < ojx::num_tiles(); ++t)
+    for (int s : kSplits)
+      if (candidate_ok(M, N, K, ojx_cfg{t, s})) {
+        if (n == idx) { *out = ojx_cfg{t, s}; return OJX_OK; }
+        ++n;
+      }
+  return fail(OJX_ERR_CONFIG, "candidate index %d out of range [0, %d)", idx, n);
+}
+
+int64_t ojx_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg) {
+  ojx_cfg c;
+  if (resolve(M, N, K, kind, cfg, &c) != OJX_OK) return -1;
+  return c.splitk > 1 ? (int64_t)c.splitk * M * N * 4 : 0;
+}
+
+int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                  int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                  ojx_stream_t stream) {
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;  // an empty tensor may have a null data pointer
+  OJX_TRY(check_operands(x, w, ldx, ldw, K));
+  if (y == nullptr || !aligned(y, 8) || ldy < N || ldy % 4 != 0)
+    return fail(OJX_ERR_ARG, "y must be 8-byte aligned with row stride >= N and a multiple of 4");
+  ojx_cfg c;
+  OJX_TRY(resolve(M, N, K, OJX_KIND_PLAIN, cfg, &c));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (c.splitk == 1) return gemm(c, ojx::EPI_BF16, x, ldx, w, ldw, y, ldy, nullptr, 0, M, N, K, st);
+  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
+  float* parts = static_cast<float*>(workspace);
+  OJX_TRY(gemm(c, ojx::EPI_F32, x, ldx, w, ldw, parts, N, nullptr, 0, M, N, K, st));
+  return hip_check(ojx::launch_reduce_bf16(parts, c.splitk, M * N, static_cast<uint16_t*>(y), ldy, (int)M, (int)N,
+                                           st), "reduce launch");
+}
+
+int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                        int64_t ldw, int32_t S, int32_t tile, ojx_stream_t stream) {
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;
+  OJX_TRY(check_operands(x, w, ldx, ldw, K));
+  if (parts == nullptr || !aligned(parts, 16)) return fail(OJX_ERR_ARG, "parts must be 16-byte aligned");
+  ojx_cfg c;
+  if (tile < 0) OJX_TRY(ojx_plan(M, N, K, OJX_KIND_RESIDUAL, &c));
+  else c.tile = tile;
+  c.splitk = S;
+  if (!cfg_fits(M, N, K, c))
+    return fail(OJX_ERR_CONFIG, "split-K S=%d (tile %d) invalid for K=%lld", S, c.tile, (long long)K);
+  return gemm(c, ojx::EPI_F32, x, ldx, w, ldw, parts, N, nullptr, 0, M, N, K, static_cast<hipStream_t>(stream));
+}
+
+int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t M, int64_t I, int64_t K,
+                      void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
+  if (I <= 0 || I % 4 != 0) return fail(OJX_ERR_SHAPE, "I (%lld) must be a positive multiple of 4", (long long)I);
+  const int64_t N = 2 * I;
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;
+  OJX_TRY(check_operands(x, w_gu_packed, K, K, K));
+  if (out == nullptr || !aligned(out, 8)) return fail(OJX_ERR_ARG, "out must be 8-byte aligned");
+  ojx_cfg c;
+  OJX_TRY(resolve(M, N, K, OJX_KIND_SILU_MUL, cfg, &c));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (c.splitk == 1) return gemm(c, ojx::EPI_SILU, x, K, w_gu_packed, K, out, I, nullptr, 0, M, N, K, st);
+  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
+  float* parts = static_cast<float*>(workspace);
+  OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w_gu_packed, K, parts, N, nullptr, 0, M, N, K, st));
+  return hip_check(ojx::launch_reduce_silu(parts, c.splitk, M * N, static_cast<uint16_t*>(out), I, (int)M, (int)N,
+                                           st), "reduce launch");
+}
+
+int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual, const float* w1,
+                              const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
+                              int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                              ojx_stream_t stream) {
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;
+  OJX_TRY(check_operands(x, w, K, K, K));
+  if (residual == nullptr || h_out == nullptr || !aligned(residual, 16) || !aligned(h_out, 16))
+    return fail(OJX_ERR_ARG, "residual and h_out must be non-null and 16-byte aligned");
+  if (hn_out != nullptr) {
+    OJX_TRY(check_rows(M, N));
+    if (w1 == nullptr || !aligned(w1, 16) || !aligned(hn_out, 16))
+      return fail(OJX_ERR_ARG, "w1 and hn_out must be non-null and 16-byte aligned");
+  }
+  if (M == 0) return OJX_OK;
+  ojx_cfg c;
+  OJX_TRY(resolve(M, N, K, OJX_KIND_RESIDUAL, cfg, &c));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  uint16_t* h = static_cast<uint16_t*>(h_out);
+  uint16_t* hn = static_cast<uint16_t*>(hn_out);
+  if (c.splitk == 1) {
+    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st));
+    if (hn == nullptr) return OJX_OK;
+    return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,
+                                             (int)N, st), "rmsnorm launch");
+  }
+  if (hn == nullptr && N / 8 > 1024) return fail(OJX_ERR_SHAPE, "split-K residual needs N/8 <= 1024");
+  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
+  float* parts = static_cast<float*>(workspace);
+  OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st));
+  return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(residual), nullptr, parts, c.splitk, M * N,
+                                           w1, rowmask, eps, h, hn, (int)M, (int)N, st), "rmsnorm launch");
+}
+
+int ojx_add_rmsnorm(const void* x, const void* delta, const float* w1, const int32_t* rowmask, float eps,
+                    void* h_out, void* hn_out, int64_t M, int64_t H, ojx_stream_t stream) {
+  OJX_TRY(check_rows(M, H));
+  if (M == 0) return OJX_OK;
+  if (x == nullptr || hn_out == nullptr || w1 == nullptr) return fail(OJX_ERR_ARG, "null x, hn_out or w1");
+  if (delta != nullptr && h_out == nullptr) return fail(OJX_ERR_ARG, "h_out required when delta is given");
+  if (!aligned(x, 16) || !aligned(hn_out, 16) || !aligned(w1, 16) || (delta && !aligned(delta, 16)) ||
+      (h_out && !aligned(h_out, 16)))
+    return fail(OJX_ERR_ARG, "row kernel operands must be 16-byte aligned");
+  if (M == 0) return OJX_OK;
+  return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(delta),
+                                           nullptr, 0, 0, w1, rowmask, eps,
+                                           delta ? static_cast<uint16_t*>(h_out) : nullptr,
+                                           static_cast<uint16_t*>(hn_out), (int)M, (int)H,
+                                           static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
+int ojx_add_rmsnorm_sk(const void* x, const float* parts, int32_t S, const float* w1, const int32_t* rowmask,
+                       float eps, void* h_out, void* hn_out, int64_t M, int64_t H, ojx_stream_t stream) {
+  OJX_TRY(check_rows(M, H));
+  if (S < 1 || S > kMaxSplit) return fail(OJX_ERR_CONFIG, "S must be in [1, %d]", kMaxSplit);
+  if (M == 0) return OJX_OK;
+  if (x == nullptr || parts == nullptr || h_out == nullptr || hn_out == nullptr || w1 == nullptr)
+    return fail(OJX_ERR_ARG, "null operand");
+  if (!aligned(x, 16) || !aligned(parts, 16) || !aligned(h_out, 16) || !aligned(hn_out, 16) || !aligned(w1, 16))
+    return fail(OJX_ERR_ARG, "row kernel operands must be 16-byte aligned");
+  if (M == 0) return OJX_OK;
+  return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(x), nullptr, parts, S, M * H, w1, rowmask,
+                                           eps, static_cast<uint16_t*>(h_out), static_cast<uint16_t*>(hn_out),
+                                           (int)M, (int)H, static_cast<hipStream_t>(stream)), "rmsnorm launch");
+}
+
+static int silu_common(const void* gu, const void* tab, void* out, int64_t M, int64_t I, ojx_stream_t stream) {
+  if (I <= 0 || I % 8 != 0 || M < 0) return fail(OJX_ERR_SHAPE, "silu_mul needs I %% 8 == 0 (I=%lld)", (long long)I);
+  if (M == 0) return OJX_OK;
+  if (gu == nullptr || out == nullptr || !aligned(gu, 16) || !aligned(out, 16))
+    return fail(OJX_ERR_ARG, "gu and out must be non-null and 16-byte aligned");
+  if (M == 0) return OJX_OK;
+  return hip_check(ojx::launch_silu_mul(static_cast<const uint16_t*>(gu), static_cast<const uint16_t*>(tab),
+                                        static_cast<uint16_t*>(out), (int)M, (int)I,
+                                        static_cast<hipStream_t>(stream)), "silu_mul launch");
+}
+
+int ojx_silu_mul(const void* gu, void* out, int64_t M, int64_t I, ojx_stream_t stream) {
+  return silu_common(gu, nullptr, out, M, I, stream);
+}
+
+int ojx_silu_mul_lut(const void* gu, const void* tab, void* out, int64_t M, int64_t I, ojx_stream_t stream) {
+  if (tab == nullptr) return fail(OJX_ERR_ARG, "null table");
+  return silu_common(gu, tab, out, M, I, stream);
+}
+
+int ojx_act_tables(void* silu_b, float* sig_f, ojx_stream_t stream) {
+  if (silu_b == nullptr || sig_f == nullptr) return fail(OJX_ERR_ARG, "null table output");
+  return hip_check(ojx::launch_act_tables(static_cast<uint16_t*>(silu_b), sig_f, static_cast<hipStream_t>(stream)),
+                   "act_tables launch");
+}
+
+int ojx_pack_gate_up(const void* gate, const void* up, void* packed, int64_t I, int64_t K, ojx_stream_t stream) {
+  if (I <= 0 || I % 4 != 0 || K <= 0 || K % 8 != 0)
+    return fail(OJX_ERR_SHAPE, "pack_gate_up needs I %% 4 == 0 and K %% 8 == 0");
+  if (gate == nullptr || up == nullptr || packed == nullptr || !aligned(gate, 16) || !aligned(up, 16) ||
+      !aligned(packed, 16))
+    return fail(OJX_ERR_ARG, "gate, up and packed must be non-null and 16-byte aligned");
+  return hip_check(ojx::launch_pack_gate_up(static_cast<const uint16_t*>(gate), static_cast<const uint16_t*>(up),
+                                            static_cast<uint16_t*>(packed), (int)I, (int)K,
+                                            static_cast<hipStream_t>(stream)), "pack launch");
+}
+
+}  // extern "C"

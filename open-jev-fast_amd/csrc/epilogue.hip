@@ -1,0 +1,215 @@
+// Second-pass and standalone epilogue kernels of the projection path (HBM-bound row / elementwise work).
+//
+//   reduce_bf16_k     y = bf16(sum_s parts[s])                                   (split-K plain projection)
+//   reduce_silu_k     out = bf16(bf16(silu(bf16 g)) * bf16 u), g/u = sum_s parts  (split-K gate-up)
+//   add_rmsnorm_k     h = bf16(x + bf16(delta)); hn = bf16((h * rsqrt(mean h^2 + eps)) * w1), 0 where rowmask == 0
+//                     delta = nothing | bf16 [M,H] | sum_s fp32 parts[s]
+//                     (reference: add_rmsnorm_k src/kernels.cu:41-73, add_rmsnorm_sk2_k src/kernels.cu:1444-1501)
+//   silu_mul_k        gu = [gate | up] row stride 2I -> out = bf16(bf16(silu(g)) * u), optionally through the
+//                     65536-entry table (reference: silu_mul_k src/kernels.cu:76-89, silu_mul_lut_k :1304-1331)
+//   act_tables_k      silu_b[bits] = bf16(silu(x)), sig_f[bits] = sigmoid(x) (reference: src/kernels.cu:1288-1301)
+//   pack_gate_up_k    W_gu rows in blocks of 8: gate rows 4b..4b+3 then up rows 4b..4b+3 (the GEMM's fused
+//                     SiLU.mul layout; the reference concatenates [gate; up], src/fastmodel.py:90)
+//
+// All loads and stores are 16-byte vectors; split partial planes are summed in ascending split order, the order
+// of add_rmsnorm_sk2_k (src/kernels.cu:1464-1468), so results do not depend on the launch.
+#include "ojx_internal.h"
+
+namespace ojx {
+
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+
+__global__ void __launch_bounds__(256) reduce_bf16_k(const float* __restrict__ parts, int S, int64_t ps,
+                                                     uint16_t* __restrict__ y, int64_t ldy, int M, int N) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int n4 = N >> 2;
+  if (idx >= (int64_t)M * n4) return;
+  const int m = (int)(idx / n4), n = (int)(idx - (int64_t)m * n4) * 4;
+  const float* src = parts + (int64_t)m * N + n;
+  float4 s = *reinterpret_cast<const float4*>(src);
+  for (int k = 1; k < S; ++k) {
+    const float4 t = *reinterpret_cast<const float4*>(src + k * ps);
+    s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
+  }
+  *reinterpret_cast<uint2*>(y + (int64_t)m * ldy + n) = make_uint2(pack2(s.x, s.y), pack2(s.z, s.w));
+}
+
+// parts: [S, M, N] with N = 2I packed as blocks of 8 (4 gate, 4 up); out: [M, I] row stride ldo.
+__global__ void __launch_bounds__(256) reduce_silu_k(const float* __restrict__ parts, int S, int64_t ps,
+                                                     uint16_t* __restrict__ out, int64_t ldo, int M, int N) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int nb = N >> 3;  // blocks of 8 packed columns = groups of 4 output columns
+  if (idx >= (int64_t)M * nb) return;
+  const int m = (int)(idx / nb), blk = (int)(idx - (int64_t)m * nb);
+  const float* src = parts + (int64_t)m * N + blk * 8;
+  float4 g = *reinterpret_cast<const float4*>(src);
+  float4 u = *reinterpret_cast<const float4*>(src + 4);
+  for (int k = 1; k < S; ++k) {
+    const float4 a = *reinterpret_cast<const float4*>(src + k * ps);
+    const float4 c = *reinterpret_cast<const float4*>(src + k * ps + 4);
+    g.x += a.x; g.y += a.y; g.z += a.z; g.w += a.w;
+    u.x += c.x; u.y += c.y; u.z += c.z; u.w += c.w;
+  }
+  const float o0 = rbf(silu_f(rbf(g.x))) * rbf(u.x), o1 = rbf(silu_f(rbf(g.y))) * rbf(u.y);
+  const float o2 = rbf(silu_f(rbf(g.z))) * rbf(u.z), o3 = rbf(silu_f(rbf(g.w))) * rbf(u.w);
+  *reinterpret_cast<uint2*>(out + (int64_t)m * ldo + blk * 4) = make_uint2(pack2(o0, o1), pack2(o2, o3));
+}
+
+// Sum over the whole workgroup (wave64 butterfly, then one value per wave through LDS).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// One workgroup per row, H/8 threads, 8 contiguous elements per thread.
+__global__ void __launch_bounds__(1024) add_rmsnorm_k(const uint16_t* __restrict__ x,
+                                                      const uint16_t* __restrict__ delta,
+                                                      const float* __restrict__ parts, int S, int64_t ps,
+                                                      const float* __restrict__ w1,
+                                                      const int32_t* __restrict__ rowmask, float eps,
+                                                      uint16_t* __restrict__ h_out, uint16_t* __restrict__ hn_out,
+                                                      int H) {
+  __shared__ float red[16];
+  const int64_t row = blockIdx.x;
+  const int i = threadIdx.x * 8;
+  const uint4 xa = *reinterpret_cast<const uint4*>(x + row * H + i);
+  const uint32_t xw[4] = {xa.x, xa.y, xa.z, xa.w};
+  float xv[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) { xv[2 * j] = bf2f(xw[j] & 0xffffu); xv[2 * j + 1] = bf2f(xw[j] >> 16); }
+  float v[8];
+  if (parts != nullptr || delta != nullptr) {
+    float d[8];
+    if (parts != nullptr) {
+      const float* pp = parts + row * H + i;
+      float4 a = *reinterpret_cast<const float4*>(pp), b = *reinterpret_cast<const float4*>(pp + 4);
+      for (int s = 1; s < S; ++s) {
+        const float4 c = *reinterpret_cast<const float4*>(pp + s * ps);
+        const float4 e = *reinterpret_cast<const float4*>(pp + s * ps + 4);
+        a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+        b.x += e.x; b.y += e.y; b.z += e.z; b.w += e.w;
+      }
+      d[0] = rbf(a.x); d[1] = rbf(a.y); d[2] = rbf(a.z); d[3] = rbf(a.w);
+      d[4] = rbf(b.x); d[5] = rbf(b.y); d[6] = rbf(b.z); d[7] = rbf(b.w);
+    } else {
+      const uint4 da = *reinterpret_cast<const uint4*>(delta + row * H + i);
+      const uint32_t dw[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) { d[2 * j] = bf2f(dw[j] & 0xffffu); d[2 * j + 1] = bf2f(dw[j] >> 16); }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = rbf(xv[j] + d[j]);
+    *reinterpret_cast<uint4*>(h_out + row * H + i) =
+        make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = xv[j];
+  }
+  if (hn_out == nullptr) return;  // uniform across the workgroup
+  const float4 wa = *reinterpret_cast<const float4*>(w1 + i), wb = *reinterpret_cast<const float4*>(w1 + i + 4);
+  const bool keep = rowmask == nullptr || rowmask[row] != 0;
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  ss = block_sum(ss, red);
+  const float r = rsqrtf(ss / (float)H + eps);
+  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = keep ? (v[j] * r) * wv[j] : 0.f;
+  *reinterpret_cast<uint4*>(hn_out + row * H + i) =
+      make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+}
+
+__global__ void __launch_bounds__(256) silu_mul_k(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ tab,
+                                                  uint16_t* __restrict__ out, int I, int64_t total8) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total8) return;
+  const int64_t e = idx * 8;
+  const int64_t row = e / I, col = e - row * I;
+  const uint4 ga = *reinterpret_cast<const uint4*>(gu + row * 2 * I + col);
+  const uint4 ua = *reinterpret_cast<const uint4*>(gu + row * 2 * I + I + col);
+  const uint32_t gw[4] = {ga.x, ga.y, ga.z, ga.w}, uw[4] = {ua.x, ua.y, ua.z, ua.w};
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t gb = (j & 1) ? (gw[j >> 1] >> 16) : (gw[j >> 1] & 0xffffu);
+    const uint32_t ub = (j & 1) ? (uw[j >> 1] >> 16) : (uw[j >> 1] & 0xffffu);
+    const float s = tab != nullptr ? bf2f(tab[gb]) : rbf(silu_f(bf2f(gb)));
+    o[j] = s * bf2f(ub);
+  }
+  *reinterpret_cast<uint4*>(out + e) =
+      make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+}
+
+__global__ void __launch_bounds__(256) act_tables_k(uint16_t* __restrict__ silu_b, float* __restrict__ sig_f) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= 65536) return;
+  const float x = bf2f((uint32_t)i);
+  silu_b[i] = (uint16_t)f2bf(silu_f(x));
+  sig_f[i] = sigmoid_f(x);
+}
+
+// packed row p: block b = p / 8, w = p % 8 -> gate row 4b + w (w < 4) or up row 4b + w - 4
+__global__ void __launch_bounds__(256) pack_gate_up_k(const uint16_t* __restrict__ gate,
+                                                      const uint16_t* __restrict__ up,
+                                                      uint16_t* __restrict__ packed, int I, int K) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int cpr = K >> 3;
+  if (idx >= (int64_t)2 * I * cpr) return;
+  const int64_t p = idx / cpr;
+  const int c = (int)(idx - p * cpr) * 8;
+  const int64_t blk = p >> 3, w = p & 7;
+  const uint16_t* src = (w < 4 ? gate : up) + (blk * 4 + (w & 3)) * K + c;
+  *reinterpret_cast<uint4*>(packed + p * K + c) = *reinterpret_cast<const uint4*>(src);
+}
+
+static inline unsigned nblocks(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
+
+hipError_t launch_reduce_bf16(const float* parts, int S, int64_t ps, uint16_t* y, int64_t ldy, int M, int N,
+                              hipStream_t st) {
+  const int64_t n = (int64_t)M * (N / 4);
+  hipLaunchKernelGGL(reduce_bf16_k, dim3(nblocks(n, 256)), dim3(256), 0, st, parts, S, ps, y, ldy, M, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_reduce_silu(const float* parts, int S, int64_t ps, uint16_t* out, int64_t ldo, int M, int N,
+                              hipStream_t st) {
+  const int64_t n = (int64_t)M * (N / 8);
+  hipLaunchKernelGGL(reduce_silu_k, dim3(nblocks(n, 256)), dim3(256), 0, st, parts, S, ps, out, ldo, M, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* delta, const float* parts, int S, int64_t ps,
+                              const float* w1, const int32_t* rowmask, float eps, uint16_t* h_out,
+                              uint16_t* hn_out, int M, int H, hipStream_t st) {
+  hipLaunchKernelGGL(add_rmsnorm_k, dim3(M), dim3(H / 8), 0, st, x, delta, parts, S, ps, w1, rowmask, eps, h_out,
+                     hn_out, H);
+  return hipGetLastError();
+}
+
+hipError_t launch_silu_mul(const uint16_t* gu, const uint16_t* tab, uint16_t* out, int M, int I, hipStream_t st) {
+  const int64_t total8 = (int64_t)M * I / 8;
+  hipLaunchKernelGGL(silu_mul_k, dim3(nblocks(total8, 256)), dim3(256), 0, st, gu, tab, out, I, total8);
+  return hipGetLastError();
+}
+
+hipError_t launch_act_tables(uint16_t* silu_b, float* sig_f, hipStream_t st) {
+  hipLaunchKernelGGL(act_tables_k, dim3(256), dim3(256), 0, st, silu_b, sig_f);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* packed, int I, int K,
+                               hipStream_t st) {
+  const int64_t n = (int64_t)2 * I * (K / 8);
+  hipLaunchKernelGGL(pack_gate_up_k, dim3(nblocks(n, 256)), dim3(256), 0, st, gate, up, packed, I, K);
+  return hipGetLastError();
+}
+
+}  // namespace ojx

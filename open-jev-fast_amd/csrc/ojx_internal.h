@@ -1,0 +1,73 @@
+// Internal declarations shared by the HIP translation units of libojx (not part of the C-ABI).
+//
+// Conventions used throughout:
+//   * bf16 values travel as raw 16-bit patterns (uint16_t); conversions are explicit and round to nearest even,
+//     which is what torch's c10::BFloat16 and CUDA's __float2bfloat16 do (reference: src/kernels.cu:12-13).
+//   * A projection computes y[M,N] = x[M,K] . W[N,K]^T with both operands K-contiguous ("NT"), the layout of
+//     the reference's lt_matmul (src/lt.cpp:22-29) and F.linear.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ojx {
+
+// ----------------------------------------------------------------------------------------------------------------
+// bf16 helpers
+__device__ __forceinline__ float bf2f(uint32_t b) { return __uint_as_float(b << 16); }
+__device__ __forceinline__ uint32_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);                                  // round to nearest, ties to even
+  return u >> 16;
+}
+__device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }  // round through bf16
+__device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
+__device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+// ----------------------------------------------------------------------------------------------------------------
+// GEMM epilogue modes (what a workgroup does with its fp32 accumulator tile)
+enum Epi : int {
+  EPI_BF16 = 0,   // y = bf16(acc)
+  EPI_F32 = 1,    // split-K partial: parts[z][m][n] = acc (fp32)
+  EPI_RESID = 2,  // h = bf16(residual + bf16(acc))
+  EPI_SILU = 3,   // packed gate/up rows -> out = bf16(bf16(silu(bf16 g)) * bf16 u)
+  EPI_COUNT = 4
+};
+
+struct GemmParams {
+  const uint16_t* W; int64_t ldw;   // [N, K] bf16, row stride ldw elements
+  const uint16_t* X; int64_t ldx;   // [M, K] bf16, row stride ldx elements
+  void* out; int64_t ldo;           // bf16 [M, N] (or [M, N/2] for EPI_SILU), or fp32 parts [S, M, N]
+  const uint16_t* res; int64_t ldr; // residual [M, N] bf16 for EPI_RESID
+  int64_t part_stride;              // elements between split-K partial planes (EPI_F32)
+  int M, N, K;
+  int kchunk;                       // K elements per split (multiple of 8; the last split may be shorter)
+  int tiles_n, tiles_m, splits;
+};
+
+struct TileInfo {
+  int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M
+  int threads;
+  int lds_bytes;
+};
+
+// Tile registry (gemm.hip)
+int num_tiles();
+hipError_t init_tiles();  // sets the dynamic-LDS limit of every tile kernel
+const TileInfo* tile_info(int tile);
+hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream);
+
+// Row / elementwise kernels (epilogue.hip)
+hipError_t launch_reduce_bf16(const float* parts, int S, int64_t part_stride, uint16_t* y, int64_t ldy,
+                              int M, int N, hipStream_t st);
+hipError_t launch_reduce_silu(const float* parts, int S, int64_t part_stride, uint16_t* out, int64_t ldo,
+                              int M, int N, hipStream_t st);
+hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* delta_bf16, const float* parts, int S,
+                              int64_t part_stride, const float* w1, const int32_t* rowmask, float eps,
+                              uint16_t* h_out, uint16_t* hn_out, int M, int H, hipStream_t st);
+hipError_t launch_silu_mul(const uint16_t* gu, const uint16_t* tab, uint16_t* out, int M, int I, hipStream_t st);
+hipError_t launch_act_tables(uint16_t* silu_b, float* sig_f, hipStream_t st);
+hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* packed, int I, int K,
+                               hipStream_t st);
+
+}  // namespace ojx

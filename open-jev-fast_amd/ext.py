@@ -1,0 +1,200 @@
+"""Projection-path functions of the reference's kernel extension `K` (src/ext.py:6-29), on libojx.
+
+Same names, arguments, return values and error behaviour (RuntimeError) as the reference's torch-extension
+functions, for the entry points on the projection path:
+
+    add_rmsnorm(x, delta, w1, rowmask, eps) -> [h, hn]        src/kernels.cu:41-73, 755-767
+    add_rmsnorm_sk(x, parts, w1, rowmask, eps) -> [h, hn]     src/kernels.cu:475-515, 886-900
+    add_rmsnorm_sk2(x, parts, w1, rowmask, eps) -> [h, hn]    src/kernels.cu:1444-1501 (S in 2..4)
+    silu_mul(gu) -> out                                       src/kernels.cu:76-89, 769-777
+    silu_mul_lut(gu, tab) -> out                              src/kernels.cu:1304-1331
+    act_tables(like) -> [silu_b, sig_f]                       src/kernels.cu:1288-1301
+
+plus the fused projections that replace GEMM + epilogue pairs (mm, mm_silu_mul, mm_residual_rmsnorm,
+mm_splitk_f32) and pack_gate_up, the weight layout of the fused gate-up.
+
+Tensors must be contiguous GPU tensors (the reference's CHECK, src/kernels.cu:10); outputs come from torch.empty on
+the current stream's device and every launch goes on torch's current stream, so all of it can be captured in a
+CUDA/HIP graph.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import KIND_PLAIN, KIND_RESIDUAL, KIND_SILU_MUL, check, lib
+
+
+def _stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _chk(t, name, dtype=None):
+    if t is None:
+        raise RuntimeError(f"{name} must be a tensor")
+    if not (t.is_cuda and t.is_contiguous()):
+        raise RuntimeError(f"{name} must be contiguous CUDA")
+    if dtype is not None and t.dtype != dtype:
+        raise RuntimeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _cfgp(cfg):
+    if cfg is None:
+        return None
+    if not isinstance(cfg, _lib.OjxCfg):
+        cfg = _lib.OjxCfg(*cfg)
+    return ctypes.byref(cfg)
+
+
+def _workspace(M, N, K, kind, cfg, device):
+    n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
+    if n < 0:
+        check(1)
+    if n == 0:
+        return None, 0
+    return torch.empty(n, dtype=torch.uint8, device=device), n
+
+
+# ------------------------------------------------------------------------------------------------ epilogues
+def add_rmsnorm(x, delta, w1, rowmask, eps):
+    _chk(x, "x", torch.bfloat16)
+    _chk(w1, "w1", torch.float32)
+    M, H = x.shape
+    hn = torch.empty_like(x)
+    if delta is not None:
+        _chk(delta, "delta", torch.bfloat16)
+        h = torch.empty_like(x)
+    else:
+        h = x
+    if rowmask is not None:
+        _chk(rowmask, "rowmask", torch.int32)
+    check(lib().ojx_add_rmsnorm(_ptr(x), _ptr(delta), _ptr(w1), _ptr(rowmask), float(eps),
+                                _ptr(h) if delta is not None else None, _ptr(hn), M, H, _stream()))
+    return [h, hn]
+
+
+def add_rmsnorm_sk(x, parts, w1, rowmask, eps):
+    _chk(x, "x", torch.bfloat16)
+    _chk(parts, "parts", torch.float32)
+    _chk(w1, "w1", torch.float32)
+    M, H = x.shape
+    S = parts.shape[0]
+    if parts.dim() != 3 or parts.shape[1] != M or parts.shape[2] != H:
+        raise RuntimeError("parts must be [S, M, H]")
+    if rowmask is not None:
+        _chk(rowmask, "rowmask", torch.int32)
+    h, hn = torch.empty_like(x), torch.empty_like(x)
+    check(lib().ojx_add_rmsnorm_sk(_ptr(x), _ptr(parts), S, _ptr(w1), _ptr(rowmask), float(eps), _ptr(h), _ptr(hn),
+                                   M, H, _stream()))
+    return [h, hn]
+
+
+def add_rmsnorm_sk2(x, parts, w1, rowmask, eps):
+    if not 2 <= parts.shape[0] <= 4:
+        raise RuntimeError("S must be 2..4")
+    return add_rmsnorm_sk(x, parts, w1, rowmask, eps)
+
+
+def silu_mul(gu):
+    _chk(gu, "gu", torch.bfloat16)
+    M, I2 = gu.shape
+    out = torch.empty((M, I2 // 2), dtype=gu.dtype, device=gu.device)
+    check(lib().ojx_silu_mul(_ptr(gu), _ptr(out), M, I2 // 2, _stream()))
+    return out
+
+
+def silu_mul_lut(gu, tab):
+    _chk(gu, "gu", torch.bfloat16)
+    _chk(tab, "tab", torch.bfloat16)
+    M, I2 = gu.shape
+    out = torch.empty((M, I2 // 2), dtype=gu.dtype, device=gu.device)
+    check(lib().ojx_silu_mul_lut(_ptr(gu), _ptr(tab), _ptr(out), M, I2 // 2, _stream()))
+    return out
+
+
+def act_tables(like):
+    silu_b = torch.empty(65536, dtype=torch.bfloat16, device=like.device)
+    sig_f = torch.empty(65536, dtype=torch.float32, device=like.device)
+    check(lib().ojx_act_tables(_ptr(silu_b), _ptr(sig_f), _stream()))
+    return [silu_b, sig_f]
+
+
+# ------------------------------------------------------------------------------------------------ projections
+def mm(x, w, cfg=None):
+    """y = x . w^T, bf16 out (the reference's _mm / lt_matmul / F.linear)."""
+    _chk(x, "x", torch.bfloat16)
+    _chk(w, "w", torch.bfloat16)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)} w {tuple(w.shape)}")
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    ws, nws = _workspace(M, N, K, KIND_PLAIN, cfg, x.device)
+    check(lib().ojx_gemm_bf16(_ptr(x), _ptr(w), _ptr(y), M, N, K, K, K, N, _ptr(ws), nws, _cfgp(cfg), _stream()))
+    return y
+
+
+def mm_splitk_f32(x, w, S, tile=-1):
+    """parts [S, M, N] fp32 over S contiguous K ranges (the reference's _skmm torch.bmm with out_dtype=fp32)."""
+    _chk(x, "x", torch.bfloat16)
+    _chk(w, "w", torch.bfloat16)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)} w {tuple(w.shape)}")
+    parts = torch.empty((S, M, N), dtype=torch.float32, device=x.device)
+    check(lib().ojx_gemm_splitk_f32(_ptr(x), _ptr(w), _ptr(parts), M, N, K, K, K, S, tile, _stream()))
+    return parts
+
+
+def mm_silu_mul(x, w_gu_packed, cfg=None):
+    """out [M, I] = bf16(bf16(silu(g)) * u), [g | u] = x . W_gu^T, W_gu in pack_gate_up layout [2I, K]."""
+    _chk(x, "x", torch.bfloat16)
+    _chk(w_gu_packed, "w_gu", torch.bfloat16)
+    M, K = x.shape
+    N = w_gu_packed.shape[0]
+    if w_gu_packed.shape[1] != K or N % 2:
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)} w_gu {tuple(w_gu_packed.shape)}")
+    out = torch.empty((M, N // 2), dtype=x.dtype, device=x.device)
+    ws, nws = _workspace(M, N, K, KIND_SILU_MUL, cfg, x.device)
+    check(lib().ojx_gemm_silu_mul(_ptr(x), _ptr(w_gu_packed), _ptr(out), M, N // 2, K, _ptr(ws), nws, _cfgp(cfg),
+                                  _stream()))
+    return out
+
+
+def mm_residual_rmsnorm(h, y, w, w1, rowmask, eps, want_hn=True, cfg=None):
+    """(h_new, hn): h_new = bf16(h + bf16(y . w^T)); hn = RMSNorm(h_new) * w1 (zero where rowmask == 0)."""
+    _chk(h, "h", torch.bfloat16)
+    _chk(y, "y", torch.bfloat16)
+    _chk(w, "w", torch.bfloat16)
+    M, K = y.shape
+    N = w.shape[0]
+    if w.shape[1] != K or tuple(h.shape) != (M, N):
+        raise RuntimeError(f"shape mismatch: h {tuple(h.shape)} y {tuple(y.shape)} w {tuple(w.shape)}")
+    if want_hn:
+        _chk(w1, "w1", torch.float32)
+    if rowmask is not None:
+        _chk(rowmask, "rowmask", torch.int32)
+    h_new = torch.empty_like(h)
+    hn = torch.empty_like(h) if want_hn else None
+    ws, nws = _workspace(M, N, K, KIND_RESIDUAL, cfg, y.device)
+    check(lib().ojx_gemm_residual_rmsnorm(_ptr(y), _ptr(w), _ptr(h), _ptr(w1) if want_hn else None, _ptr(rowmask),
+                                          float(eps), _ptr(h_new), _ptr(hn), M, N, K, _ptr(ws), nws, _cfgp(cfg),
+                                          _stream()))
+    return h_new, hn
+
+
+def pack_gate_up(gate, up):
+    """W_gu for mm_silu_mul: [2I, K], rows in blocks of 8 (4 gate rows, then the same 4 up rows)."""
+    _chk(gate, "gate", torch.bfloat16)
+    _chk(up, "up", torch.bfloat16)
+    if gate.shape != up.shape:
+        raise RuntimeError("gate and up must have the same shape")
+    I, K = gate.shape
+    packed = torch.empty((2 * I, K), dtype=gate.dtype, device=gate.device)
+    check(lib().ojx_pack_gate_up(_ptr(gate), _ptr(up), _ptr(packed), I, K, _stream()))
+    return packed

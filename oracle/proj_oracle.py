@@ -1,0 +1,136 @@
+"""CPU oracle of the dense bf16 projection path — TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and only as the
+checker or the reported CPU baseline; the product path (libojx.so and the open-jev-fast_amd package) never calls it.
+
+What it restates (reference file:line):
+  linear_bf16        y = bf16(x . W^T), fp32 accumulation: lt_matmul's CUBLAS_COMPUTE_32F with bf16 in/out
+                     (src/lt.cpp:22-29, 43-55), F.linear in _mm (src/fastmodel.py:168-175); BASELINE names
+                     "torch bf16 matmul (fp32 accumulate)" as the oracle, so this is torch.matmul on fp32 copies.
+  splitk_parts       parts[s] = x[:, K_s] . W[:, K_s]^T in fp32 (torch.bmm out_dtype=fp32, src/fastmodel.py:166)
+  silu_mul           out = bf16(bf16(silu(g)) * u), gu = [g | u] (src/kernels.cu:76-89; LUT form :1288-1331)
+  add_rmsnorm        h = bf16(x + bf16(delta)); hn = bf16((h * rsqrt(sum h^2 / H + eps)) * w1), 0 if rowmask == 0
+                     (src/kernels.cu:41-73); with fp32 partials delta = bf16(sum_s parts[s]), s ascending
+                     (add_rmsnorm_sk2_k, src/kernels.cu:1444-1501)
+  residual_proj      _res (src/fastmodel.py:196-203) = splitk_parts + add_rmsnorm with partials
+  gate_up_silu       _silu_mul(_mm(hn, cat[gate; up])) (src/fastmodel.py:90, 478, 190-194)
+  pack_gate_up       the fused-GEMM weight layout (rows in blocks of 8: 4 gate rows, 4 up rows) — libojx's own
+                     layout, restated here so tests can build it on the CPU
+  linear_f64         fp64 brute-force dot products (numpy), the independent check the oracle is pinned against
+
+Pinning (tests/test_oracle.py): linear_bf16 against linear_f64 and exact closed forms (identity, permutation,
+exactly representable rank-1 products); silu_mul against scipy's expit in fp64 and special values; add_rmsnorm
+against an fp64 RMSNorm and closed-form constant rows; the gate/up merge bit-exactness of tests/test_correct.py:44;
+splitk_parts summing to linear_f64. The reference holds no golden vectors for this path (no fixtures in its tree);
+tests/golden/ holds fp64 brute-force vectors made by tests/golden/make_golden.py.
+"""
+import numpy as np
+import torch
+
+
+def _bf16(t):
+    return t.to(torch.bfloat16)
+
+
+def linear_bf16(x, w):
+    """bf16(x . w^T) with fp32 accumulation on the CPU (x [M,K], w [N,K] bf16)."""
+    return _bf16(torch.matmul(x.float(), w.float().t()))
+
+
+def linear_f32(x, w):
+    return torch.matmul(x.float(), w.float().t())
+
+
+def linear_f64(x, w):
+    """fp64 brute force (numpy), independent of torch's GEMM."""
+    xa = x.float().numpy().astype(np.float64)
+    wa = w.float().numpy().astype(np.float64)
+    return xa @ wa.T
+
+
+def split_ranges(K, S):
+    """K ranges of the S splits: chunk = ceil(K/S) rounded up to a multiple of 8 (equal K/S chunks, as the
+    reference's x.view(M, S, K/S), whenever K is a multiple of 8*S)."""
+    c = -(-K // S)
+    c = -(-c // 8) * 8
+    return [(s * c, min(K, (s + 1) * c)) for s in range(S)]
+
+
+def splitk_parts(x, w, S):
+    """[S, M, N] fp32 partial products over the split K ranges."""
+    K = x.shape[1]
+    return torch.stack([linear_f32(x[:, a:b], w[:, a:b]) for a, b in split_ranges(K, S)])
+
+
+def silu_mul(gu):
+    """gu [M, 2I] bf16 -> bf16(bf16(silu(g)) * u)."""
+    I = gu.shape[1] // 2
+    g, u = gu[:, :I].float(), gu[:, I:].float()
+    s = _bf16(g / (1.0 + torch.exp(-g))).float()
+    return _bf16(s * u)
+
+
+def act_tables():
+    """65536-entry tables indexed by the bf16 bit pattern: silu_b bf16, sig_f fp32."""
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16)
+    x = bits.view(torch.bfloat16).float()
+    return _bf16(x / (1.0 + torch.exp(-x))), 1.0 / (1.0 + torch.exp(-x))
+
+
+def add_rmsnorm(x, delta, w1, rowmask, eps, parts=None):
+    """(h, hn) of add_rmsnorm / add_rmsnorm_sk2. delta bf16 [M,H] or None; parts fp32 [S,M,H] or None."""
+    xf = x.float()
+    if parts is not None:
+        d = _bf16(parts.float().sum(0)).float()  # ascending s, fp32
+        v = _bf16(xf + d).float()
+    elif delta is not None:
+        v = _bf16(xf + delta.float()).float()
+    else:
+        v = xf
+    H = x.shape[1]
+    ss = (v * v).sum(1, keepdim=True)
+    r = torch.rsqrt(ss / H + eps)
+    hn = _bf16((v * r) * w1.float()[None, :])
+    if rowmask is not None:
+        hn = torch.where(rowmask[:, None] != 0, hn, torch.zeros_like(hn))
+    h = _bf16(v) if (parts is not None or delta is not None) else x
+    return h, hn
+
+
+def residual_proj(residual, y, w, w1, rowmask, eps, S=1):
+    """_res: (h, hn) after the out / down projection of y with W [N, K]."""
+    parts = splitk_parts(y, w, S)
+    return add_rmsnorm(residual, None, w1, rowmask, eps, parts=parts)
+
+
+def gate_up_silu(x, w_gate, w_up):
+    """The reference's MLP front: SiLU.mul of the merged gate-up GEMM."""
+    gu = linear_bf16(x, torch.cat([w_gate, w_up], 0))
+    return silu_mul(gu)
+
+
+def pack_gate_up(gate, up):
+    """[2I, K]: rows in blocks of 8 = gate rows 4b..4b+3 then up rows 4b..4b+3."""
+    I, K = gate.shape
+    return torch.stack([gate.view(I // 4, 4, K), up.view(I // 4, 4, K)], 1).reshape(2 * I, K)
+
+
+# ---------------------------------------------------------------------------------------------- inputs
+def seeded_inputs(M, N, K, seed=0, x_std=1.0, w_std=0.02):
+    """x ~ N(0, x_std^2) [M,K], W ~ N(0, w_std^2) [N,K], both bf16."""
+    g = torch.Generator().manual_seed(seed)
+    x = _bf16(torch.randn(M, K, generator=g) * x_std)
+    w = _bf16(torch.randn(N, K, generator=g) * w_std)
+    return x, w
+
+
+def tolerance_ok(out, ref, max_rel=1e-2, mean_abs_rms=1e-3):
+    """The north-star tolerance: max |d| / max |ref| <= 1e-2 and mean |d| <= 1e-3 * RMS(ref).
+    Returns (ok, max_rel, mean_abs / rms)."""
+    o, r = out.float(), ref.float()
+    d = (o - r).abs()
+    mx = r.abs().max().clamp_min(1e-30)
+    rms = r.pow(2).mean().sqrt().clamp_min(1e-30)
+    a, b = (d.max() / mx).item(), (d.mean() / rms).item()
+    ok = bool(torch.isfinite(o).all()) and a <= max_rel and b <= mean_abs_rms
+    return ok, a, b

@@ -1,0 +1,120 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function include/ojx.h declares, and its host
+logic (plan table, candidate list, workspace sizes, argument validation and error messages) behaves."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    text = open(os.path.join(ROOT, "include", "ojx.h")).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\**(ojx_\w+)\s*\(", text, re.M)))
+
+
+def test_header_symbols_exported(pkg):
+    names = header_functions()
+    assert len(names) >= 19
+    L = ctypes.CDLL(pkg._lib.LIB_PATH)
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(pkg._lib.EXPORTS), "ctypes table out of sync with include/ojx.h"
+
+
+def test_version_and_tiles(pkg):
+    L = pkg._lib.lib()
+    assert b"gfx950" in L.ojx_version()
+    n = L.ojx_num_tiles()
+    assert n >= 8
+    for t in range(n):
+        info = pkg._lib.tile_info(t)
+        assert info["bn"] % 16 == 0 and info["bm"] % 16 == 0 and info["bk"] % 32 == 0
+        assert info["threads"] == 64 * info["wn"] * info["wm"]
+    with pytest.raises(RuntimeError, match="out of range"):
+        pkg._lib.tile_info(n)
+
+
+SHAPES = [(M, N, K) for M in (1, 7, 16, 64, 128, 288, 539, 1024, 2048)
+          for N, K in ((14336, 5120), (34816, 5120), (5120, 17408), (5120, 6144), (16384, 5120), (16480, 5120))]
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_plan_valid_for_every_contract_shape(pkg, kind):
+    L = pkg._lib.lib()
+    for M, N, K in SHAPES:
+        c = pkg._lib.plan(M, N, K, kind)
+        assert 0 <= c.tile < L.ojx_num_tiles() and 1 <= c.splitk <= 16
+        ws = pkg._lib.workspace_bytes(M, N, K, kind)
+        assert ws == (c.splitk * M * N * 4 if c.splitk > 1 else 0)
+
+
+def test_candidates(pkg):
+    cands = pkg._lib.candidates(288, 5120, 5120)
+    assert len(cands) > 10
+    assert len({(c.tile, c.splitk) for c in cands}) == len(cands)
+    # no tile whose x rows are mostly padding at M = 7
+    for c in pkg._lib.candidates(7, 5120, 5120):
+        assert pkg._lib.tile_info(c.tile)["bm"] == 16
+    L = pkg._lib.lib()
+    c = pkg._lib.OjxCfg()
+    assert L.ojx_candidate(7, 5120, 5120, 0, 10 ** 6, ctypes.byref(c)) == 4
+    assert b"out of range" in L.ojx_last_error()
+
+
+def test_argument_validation_without_gpu(pkg):
+    """These return before any HIP call, so they run on a machine without a GPU."""
+    L = pkg._lib.lib()
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    # N not a multiple of 8
+    assert L.ojx_gemm_bf16(p, p, p, 4, 60, 64, 64, 64, 60, None, 0, None, None) == 2
+    assert b"multiples of 8" in L.ojx_last_error()
+    # null operand
+    assert L.ojx_gemm_bf16(None, p, p, 4, 64, 64, 64, 64, 64, None, 0, None, None) == 1
+    # misaligned
+    mis = ctypes.c_void_p(p.value + 2)
+    assert L.ojx_gemm_bf16(mis, p, p, 4, 64, 64, 64, 64, 64, None, 0, None, None) == 1
+    # stride smaller than K
+    assert L.ojx_gemm_bf16(p, p, p, 4, 64, 64, 32, 64, 64, None, 0, None, None) == 1
+    # bad config
+    bad = pkg._lib.OjxCfg(999, 1)
+    assert L.ojx_gemm_bf16(p, p, p, 4, 64, 64, 64, 64, 64, None, 0, ctypes.byref(bad), None) == 4
+    bad = pkg._lib.OjxCfg(0, 17)
+    assert L.ojx_gemm_bf16(p, p, p, 4, 64, 64, 64, 64, 64, None, 0, ctypes.byref(bad), None) == 4
+    # split-K without workspace
+    sk = pkg._lib.OjxCfg(0, 2)
+    assert L.ojx_gemm_bf16(p, p, p, 4, 64, 64, 64, 64, 64, None, 0, ctypes.byref(sk), None) == 3
+    assert b"workspace" in L.ojx_last_error()
+    # RMSNorm row limit (H/8 <= 1024), as the reference's TORCH_CHECK (src/kernels.cu:757)
+    assert L.ojx_add_rmsnorm(p, None, p, None, 1e-6, None, p, 4, 8200, None) == 2
+    assert L.ojx_add_rmsnorm_sk(p, p, 17, p, None, 1e-6, p, p, 4, 64, None) == 4
+    # silu_mul needs I % 8 == 0
+    assert L.ojx_silu_mul(p, p, 4, 12, None) == 2
+    assert L.ojx_gemm_silu_mul(p, p, p, 4, 6, 64, None, 0, None, None) == 2
+    assert L.ojx_pack_gate_up(p, p, p, 6, 64, None) == 2
+    # M == 0 is a no-op
+    assert L.ojx_gemm_bf16(p, p, p, 0, 64, 64, 64, 64, 64, None, 0, None, None) == 0
+
+
+def test_python_mirror_errors_without_gpu(pkg):
+    import torch
+    from importlib import import_module
+    ext = import_module("open_jev_fast_amd.ext")
+    x = torch.zeros(4, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="contiguous CUDA"):
+        ext.mm(x, x)
+    with pytest.raises(RuntimeError, match="S must be 2..4"):
+        ext.add_rmsnorm_sk2(x, torch.zeros(5, 4, 64), torch.ones(64), None, 1e-6)
+    lt = import_module("open_jev_fast_amd.lt_ext").load()
+    assert lt.lt_setup(288, 5120, 5120, 8) == 8
+    with pytest.raises(RuntimeError, match="lt_setup not called"):
+        lt.lt_matmul(torch.zeros(3, 64, dtype=torch.bfloat16), torch.zeros(64, 64, dtype=torch.bfloat16), 0)
+    with pytest.raises(RuntimeError, match="fp32"):
+        lt.lt2_plan(288, 5120, 6144, 2, 0, 1)
+    h = lt.lt2_plan(288, 5120, 6144, 2, 1, 1)
+    n = lt.lt2_search(h, 400, 3)
+    assert n >= 1 and lt.lt2_info(h, 0)[1] == 2
+    raw = lt.lt2_raw(h, 0)
+    assert lt.lt2_add_raw(h, raw) == n

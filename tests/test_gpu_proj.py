@@ -1,0 +1,247 @@
+"""GPU parity of the projection kernels against the CPU oracle, through the C-ABI (libojx.so via ctypes).
+
+Tolerance: max |out - ref| / max |ref| <= 1e-2 and mean |out - ref| <= 1e-3 * RMS(ref).
+Integer-like invariants (gate/up merge, tile invariance, determinism, graph replays) are checked bit-exactly.
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(max_rel=1e-2, mean_abs_rms=1e-3)
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _tiles(pkg):
+    return range(pkg._lib.lib().ojx_num_tiles())
+
+
+def _assert_tol(O, out, ref, what):
+    ok, a, b = O.tolerance_ok(out.float().cpu(), ref.float().cpu(), **TOL)
+    assert ok, f"{what}: max_rel {a:.3e} mean/rms {b:.3e}"
+
+
+# ----------------------------------------------------------------------------------------------- plain GEMM
+SMALL = [(1, 64, 64), (7, 128, 256), (16, 256, 512), (37, 200, 328), (96, 520, 640), (288, 512, 1024),
+         (300, 264, 136)]
+
+
+@pytest.mark.parametrize("M,N,K", SMALL)
+def test_mm_every_tile_vs_oracle(pkg, ext, O, dev, M, N, K):
+    x, w = O.seeded_inputs(M, N, K, seed=M + N + K)
+    ref = O.linear_bf16(x, w)
+    xd, wd = x.to(dev), w.to(dev)
+    for t in _tiles(pkg):
+        for S in (1, 3):
+            _say(f"case mm M={M} N={N} K={K} tile={t} S={S}")
+            y = ext.mm(xd, wd, cfg=(t, S))
+            _assert_tol(O, y, ref, f"tile {t} S {S}")
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 512), (288, 1024, 2048)])
+def test_mm_planned_and_f64(pkg, ext, O, dev, M, N, K):
+    _say(f"case mm planned M={M} N={N} K={K}")
+    x, w = O.seeded_inputs(M, N, K, seed=1)
+    y = ext.mm(x.to(dev), w.to(dev)).cpu()
+    ref64 = torch.from_numpy(O.linear_f64(x, w))
+    # fp32 accumulation + one bf16 rounding: within 1 bf16 ulp of the exact value (+ small fp32 slack)
+    err = (y.double() - ref64).abs()
+    assert bool((err <= ref64.abs() * 2.0 ** -8 + 1e-4).all()), f"max err {err.max().item():.3e}"
+
+
+def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
+    """Without split-K every tile sums K in the same order: outputs are bit-identical across tiles and runs."""
+    M, N, K = 96, 512, 1024
+    x, w = O.seeded_inputs(M, N, K, seed=3)
+    xd, wd = x.to(dev), w.to(dev)
+    _say("case tile invariance")
+    base = ext.mm(xd, wd, cfg=(0, 1))
+    for t in _tiles(pkg):
+        assert torch.equal(ext.mm(xd, wd, cfg=(t, 1)), base), f"tile {t}"
+    for S in (2, 4):
+        a = ext.mm(xd, wd, cfg=(6, S))
+        assert torch.equal(a, ext.mm(xd, wd, cfg=(6, S))), "split-K not deterministic"
+
+
+def test_golden_vectors(pkg, ext, O, dev):
+    import numpy as np, os
+    path = os.path.join(os.path.dirname(__file__), "golden", "proj_golden.npz")
+    z = np.load(path)
+    for name in sorted({k.split("__")[0] for k in z.files}):
+        x = torch.from_numpy(z[f"{name}__x"].view(np.int16)).view(torch.bfloat16)
+        w = torch.from_numpy(z[f"{name}__w"].view(np.int16)).view(torch.bfloat16)
+        ref = torch.from_numpy(z[f"{name}__y64"])
+        _say(f"case golden {name} {tuple(x.shape)} x {tuple(w.shape)}")
+        y = ext.mm(x.to(dev), w.to(dev)).cpu().double()
+        err = (y - ref).abs()
+        assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-4).all()), f"{name}: max err {err.max().item():.3e}"
+
+
+def test_mm_strided_and_errors(pkg, ext, O, dev):
+    _say("case error paths")
+    x, w = O.seeded_inputs(8, 64, 64)
+    with pytest.raises(RuntimeError):
+        ext.mm(x.to(dev), w[:, :56].contiguous().to(dev))  # K mismatch
+    with pytest.raises(RuntimeError):
+        ext.mm(x.to(dev), torch.zeros(60, 64, dtype=torch.bfloat16, device=dev))  # N % 8
+    with pytest.raises(RuntimeError):
+        ext.mm(x.to(dev), w.to(dev), cfg=(999, 1))
+    with pytest.raises(RuntimeError):
+        ext.mm(x.to(dev).t(), w.to(dev))  # not contiguous
+    y = ext.mm(torch.empty(0, 64, dtype=torch.bfloat16, device=dev), w.to(dev))
+    assert y.shape == (0, 64)
+
+
+# ----------------------------------------------------------------------------------------------- gate-up
+@pytest.mark.parametrize("M,I,K", [(1, 64, 128), (7, 256, 512), (64, 512, 512), (288, 264, 384)])
+def test_mm_silu_mul_vs_oracle(pkg, ext, O, dev, M, I, K):
+    g = torch.Generator().manual_seed(M * 7 + I)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    ref = O.gate_up_silu(x, wg, wu)
+    packed = ext.pack_gate_up(wg.to(dev), wu.to(dev))
+    assert torch.equal(packed.cpu(), O.pack_gate_up(wg, wu))
+    for t in _tiles(pkg):
+        for S in (1, 2):
+            _say(f"case silu M={M} I={I} K={K} tile={t} S={S}")
+            out = ext.mm_silu_mul(x.to(dev), packed, cfg=(t, S))
+            _assert_tol(O, out, ref, f"tile {t} S {S}")
+
+
+def test_gate_up_merge_and_fusion_bitexact(pkg, ext, O, dev):
+    """tests/test_correct.py:44-45: merged gate+up == two GEMMs and silu_mul == act(gate)*up, bit-exact; the fused
+    epilogue equals GEMM -> bf16 -> silu_mul bit-exactly (same K order, same rounding points)."""
+    M, I, K = 96, 512, 1024
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16().to(dev)
+    wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16().to(dev)
+    _say("case gate-up merge")
+    gu = ext.mm(x, torch.cat([wg, wu], 0).contiguous(), cfg=(6, 1))
+    assert torch.equal(gu[:, :I], ext.mm(x, wg, cfg=(6, 1)))
+    assert torch.equal(gu[:, I:], ext.mm(x, wu, cfg=(6, 1)))
+    fused = ext.mm_silu_mul(x, ext.pack_gate_up(wg, wu), cfg=(6, 1))
+    assert torch.equal(fused, ext.silu_mul(gu))
+    tab, _ = ext.act_tables(x)
+    assert torch.equal(ext.silu_mul_lut(gu, tab), ext.silu_mul(gu))
+
+
+# ----------------------------------------------------------------------------------------------- residual
+@pytest.mark.parametrize("M,N,K", [(7, 256, 512), (64, 512, 1024), (288, 640, 2176)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_mm_residual_rmsnorm_vs_oracle(pkg, ext, O, dev, M, N, K, masked):
+    g = torch.Generator().manual_seed(M + N)
+    y = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.01).bfloat16()
+    res = torch.randn(M, N, generator=g).bfloat16()
+    w1 = (1.0 + 0.1 * torch.randn(N, generator=g)).float()
+    mask = (torch.rand(M, generator=g) > 0.3).int() if masked else None
+    eps = 1e-6
+    for t in (0, 4, 6, 10):
+        for S in (1, 2, 4):
+            _say(f"case residual M={M} N={N} K={K} tile={t} S={S} masked={masked}")
+            h, hn = ext.mm_residual_rmsnorm(res.to(dev), y.to(dev), w.to(dev), w1.to(dev),
+                                            mask.to(dev) if masked else None, eps, cfg=(t, S))
+            rh, rhn = O.residual_proj(res, y, w, w1, mask, eps, S=S)
+            _assert_tol(O, h, rh, f"h tile {t} S {S}")
+            _assert_tol(O, hn, rhn, f"hn tile {t} S {S}")
+            if masked:
+                assert bool((hn.cpu()[mask == 0] == 0).all())
+
+
+def test_splitk_parts_match_reference_chunks(pkg, ext, O, dev):
+    """mm_splitk_f32 planes equal the reference's equal-K/S chunks (K % (8 S) == 0) within fp32 noise."""
+    M, N, K, S = 64, 256, 2048, 4
+    x, w = O.seeded_inputs(M, N, K, seed=5)
+    _say("case splitk planes")
+    parts = ext.mm_splitk_f32(x.to(dev), w.to(dev), S).cpu()
+    xs = x.float().view(M, S, K // S).transpose(0, 1)
+    ws = w.float().view(N, S, K // S).permute(1, 2, 0)
+    ref = torch.bmm(xs, ws)
+    assert (parts - ref).abs().max().item() <= 1e-4 * ref.abs().max().item() + 1e-5
+
+
+# ----------------------------------------------------------------------------------------------- epilogues
+def test_add_rmsnorm_variants(pkg, ext, O, dev):
+    M, H = 33, 5120
+    g = torch.Generator().manual_seed(2)
+    x = torch.randn(M, H, generator=g).bfloat16()
+    d = (torch.randn(M, H, generator=g) * 0.5).bfloat16()
+    parts = torch.randn(3, M, H, generator=g).float()
+    w1 = (1.0 + 0.1 * torch.randn(H, generator=g)).float()
+    mask = (torch.arange(M) % 3 != 0).int()
+    _say("case add_rmsnorm")
+    h, hn = ext.add_rmsnorm(x.to(dev), d.to(dev), w1.to(dev), mask.to(dev), 1e-6)
+    rh, rhn = O.add_rmsnorm(x, d, w1, mask, 1e-6)
+    assert torch.equal(h.cpu(), rh)  # bf16(x + delta) is exact arithmetic + one rounding
+    _assert_tol(O, hn, rhn, "hn")
+    h0, hn0 = ext.add_rmsnorm(x.to(dev), None, w1.to(dev), None, 1e-6)
+    assert h0.data_ptr() == x.to(dev).data_ptr() or torch.equal(h0.cpu(), x)
+    _assert_tol(O, hn0, O.add_rmsnorm(x, None, w1, None, 1e-6)[1], "hn no delta")
+    h2, hn2 = ext.add_rmsnorm_sk2(x.to(dev), parts.to(dev), w1.to(dev), None, 1e-6)
+    rh2, rhn2 = O.add_rmsnorm(x, None, w1, None, 1e-6, parts=parts)
+    diff = (h2.cpu().float() - rh2.float()).abs()
+    assert (diff == 0).float().mean().item() > 0.999  # fp32 sum order is the same; rounding ties aside
+    _assert_tol(O, hn2, rhn2, "hn sk2")
+    with pytest.raises(RuntimeError):
+        ext.add_rmsnorm_sk2(x.to(dev), torch.zeros(5, M, H, device=dev), w1.to(dev), None, 1e-6)
+
+
+def test_silu_tables(pkg, ext, O, dev):
+    _say("case act_tables")
+    silu_b, sig_f = ext.act_tables(torch.empty(1, device=dev))
+    rs, rg = O.act_tables()
+    a, b = silu_b.cpu().view(torch.int16).int(), rs.view(torch.int16).int()
+    fin = torch.isfinite(rs.float())
+    close = ((a - b).abs() <= 1) | ~fin
+    assert bool(close.all())
+    assert (a[fin] == b[fin]).float().mean().item() > 0.999
+    fin32 = torch.isfinite(rg)
+    assert torch.allclose(sig_f.cpu()[fin32], rg[fin32], rtol=2e-6, atol=1e-30)
+
+
+# ----------------------------------------------------------------------------------------------- graphs
+def test_graph_capture_replays(pkg, ext, O, dev):
+    """Capture the four projections of one layer into a graph; every replay equals the eager result."""
+    M, K, N_in, I = 64, 512, 1024, 256
+    g = torch.Generator().manual_seed(9)
+    hn = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    h = torch.randn(M, K, generator=g).bfloat16().to(dev)
+    w_in = (torch.randn(N_in, K, generator=g) * 0.02).bfloat16().to(dev)
+    w_out = (torch.randn(K, N_in, generator=g) * 0.02).bfloat16().to(dev)
+    w_gu = ext.pack_gate_up((torch.randn(I, K, generator=g) * 0.02).bfloat16().to(dev),
+                            (torch.randn(I, K, generator=g) * 0.02).bfloat16().to(dev))
+    w_dn = (torch.randn(K, I, generator=g) * 0.02).bfloat16().to(dev)
+    w1 = torch.ones(K, device=dev)
+
+    def body():
+        proj = ext.mm(hn, w_in)
+        h1, hn1 = ext.mm_residual_rmsnorm(h, proj, w_out, w1, None, 1e-6, cfg=(4, 2))
+        m = ext.mm_silu_mul(hn1, w_gu, cfg=(4, 2))
+        return ext.mm_residual_rmsnorm(h1, m, w_dn, w1, None, 1e-6, cfg=(4, 1))
+
+    _say("case graph eager")
+    eager = [t.clone() for t in body()]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        body()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("case graph capture")
+    with torch.cuda.graph(graph):
+        outs = body()
+    for r in range(4):
+        _say(f"case graph replay {r}")
+        graph.replay()
+        torch.cuda.synchronize()
+        for a, b in zip(outs, eager):
+            assert torch.equal(a, b), f"replay {r} differs"
+        junk = ext.mm(hn, w_in)  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
