@@ -20,6 +20,8 @@ HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # must not run. The host pass warns that it does not know the feature; that warning is expected.
 FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+         # the fragment epilogues must unroll completely, or the accumulator array is left in scratch memory
+         "-mllvm", "-pragma-unroll-threshold=1000000",
          f"-I{INCLUDE}", f"-I{CSRC}"]
 
 

@@ -25,6 +25,70 @@ namespace ojx {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Buffer loads: the descriptor's byte range makes out-of-range lanes read zeros without a branch, so predicated
+// tile loads stay in flight (a branch around each load would make the compiler drain the load queue at the join).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
+  const int32_t n = bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor's range: the load returns zeros
+
+// 16-byte global -> LDS DMA: lane i of the wave writes lds + 16 i. (Kept out of the kernel templates: written
+// inline there, the address-space cast stops the host pass from emitting the kernels' launch stubs.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// Workgroup barrier that orders LDS only. __syncthreads() is a full workgroup fence, which on gfx9 waits for every
+// outstanding global load (vmcnt(0)) and would drain the weight prefetch queue at each x-tile handoff.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+
+// Epilogue of one 16x16 accumulator fragment: lane holds v[e] = y[m][n + e] (n a multiple of 4).
+__device__ __forceinline__ void store_tile(const GemmParams& p, const int epi, const int z, const int m, const int n,
+                                           const int lg, const f32x4 v) {
+  if (epi == EPI_SILU) {
+    // Packed W_gu rows come in blocks of 8: 4 gate rows then the 4 up rows of the same columns, so lane
+    // group lg (even) holds gate columns and lane group lg+1 the matching up columns.
+    const float u0 = __shfl_xor(v[0], 16), u1 = __shfl_xor(v[1], 16);
+    const float u2 = __shfl_xor(v[2], 16), u3 = __shfl_xor(v[3], 16);
+    if ((lg & 1) == 0 && m < p.M && n < p.N) {
+      const float g[4] = {v[0], v[1], v[2], v[3]};
+      const float u[4] = {u0, u1, u2, u3};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(g[e]))) * rbf(u[e]));
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
+      *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    }
+  } else if (m < p.M && n < p.N) {
+    if (epi == EPI_F32) {
+      float* dst = reinterpret_cast<float*>(p.out) + z * p.part_stride + (int64_t)m * p.ldo + n;
+      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+    } else {
+      uint32_t o[4];
+      if (epi == EPI_RESID) {
+        const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
+        const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = f2bf(rv[e] + rbf(v[e]));
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = f2bf(v[e]);
+      }
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
+      *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    }
+  }
+}
+
 template <int BN, int BM, int BK, int WN, int WM>
 __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams p, const int epi) {
   constexpr int NT = 64 * WN * WM;
@@ -41,7 +105,8 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
   uint16_t* sW = smem;               // [2][BN][LS]
   uint16_t* sX = smem + 2 * BN * LS; // [2][BM][LS]
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (lets the compiler use SGPRs)
   const int wn = wave % WN, wm = wave / WN;
   const int lr = lane & 15, lg = lane >> 4;
 
@@ -59,27 +124,24 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
   const int ke = min(p.K, kb + p.kchunk);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
+  // descriptors cover this tile's rows only: rows past N (or M) read zeros
+  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
   uint4 rw[CW], rx[CX];
   auto gload = [&](int k0) {
 #pragma unroll
     for (int i = 0; i < CW; ++i) {
       const int c = tid + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
-      const int n = n0 + row, k = k0 + col;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if ((W_CH % NT == 0 || c < W_CH) && n < p.N && k < ke)
-        v = *reinterpret_cast<const uint4*>(p.W + (int64_t)n * p.ldw + k);
-      rw[i] = v;
+      const bool ok = (W_CH % NT == 0 || c < W_CH) && k0 + col < ke;
+      rw[i] = bload(rsW, ok ? (uint32_t)(row * p.ldw + k0 + col) * 2u : kOOB);
     }
 #pragma unroll
     for (int i = 0; i < CX; ++i) {
       const int c = tid + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
-      const int m = m0 + row, k = k0 + col;
-      uint4 v = make_uint4(0u, 0u, 0u, 0u);
-      if ((X_CH % NT == 0 || c < X_CH) && m < p.M && k < ke)
-        v = *reinterpret_cast<const uint4*>(p.X + (int64_t)m * p.ldx + k);
-      rx[i] = v;
+      const bool ok = (X_CH % NT == 0 || c < X_CH) && k0 + col < ke;
+      rx[i] = bload(rsX, ok ? (uint32_t)(row * p.ldx + k0 + col) * 2u : kOOB);
     }
   };
   auto lstore = [&](int buf) {
@@ -106,7 +168,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
   if (nk > 0) {
     gload(kb);
     lstore(0);
-    __syncthreads();
+    lds_barrier();
   }
   for (int t = 0; t < nk; ++t) {
     const int buf = t & 1;
@@ -126,7 +188,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
         for (int j = 0; j < FM; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], bx[j], acc[i][j], 0, 0, 0);
     }
     if (t + 1 < nk) lstore(buf ^ 1);
-    __syncthreads();
+    lds_barrier();
   }
 
   // ---------------------------------------------------------------------------------------------- epilogue
@@ -137,40 +199,276 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
     for (int j = 0; j < FM; ++j) {
       const int n = n0 + (wn * FN + i) * 16 + lg * 4;
       const int m = m0 + (wm * FM + j) * 16 + lr;
-      const f32x4 v = acc[i][j];
-      if (epi == EPI_SILU) {
-        // Packed W_gu rows come in blocks of 8: 4 gate rows then the 4 up rows of the same columns, so lane
-        // group lg (even) holds gate columns and lane group lg+1 the matching up columns.
-        const float u0 = __shfl_xor(v[0], 16), u1 = __shfl_xor(v[1], 16);
-        const float u2 = __shfl_xor(v[2], 16), u3 = __shfl_xor(v[3], 16);
-        if ((lg & 1) == 0 && m < p.M && n < p.N) {
-          const float g[4] = {v[0], v[1], v[2], v[3]};
-          const float u[4] = {u0, u1, u2, u3};
-          uint32_t o[4];
+      store_tile(p, epi, z, m, n, lg, acc[i][j]);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------ W-direct
+// Weight-streaming variant. Each wave owns FN 16-row slabs of W and loads them from HBM straight into MFMA
+// operand registers, D k-steps (of 32) ahead through a register ring; W never passes through LDS. The x tile
+// (BM = 16 FM rows, shared by the NW waves of the workgroup) is staged global -> registers -> LDS in stages of
+// BKX k, double-buffered, the next stage's loads in flight during the current stage. LDS traffic per MFMA is
+// then one x fragment read per FN MFMAs, and the HBM stream (W) has D * FN * 1 KiB in flight per wave.
+template <int FN, int FM, int NW, int D, int BKX>
+__global__ void __launch_bounds__(64 * NW) gemm_wd_kernel(const GemmParams p, const int epi) {
+  constexpr int NT = 64 * NW;
+  constexpr int BN = NW * FN * 16, BM = FM * 16;
+  constexpr int SPS = BKX / 32;  // k32 steps per x stage
+  static_assert(BKX % 32 == 0 && (SPS % D == 0 || D % SPS == 0), "ring depth and x stage must nest");
+  constexpr int LS = BKX + 8;
+  constexpr int CPR = BKX / 8;
+  constexpr int X_CH = BM * CPR;
+  constexpr int CX = (X_CH + NT - 1) / NT;
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* sX = smem;  // [2][BM][LS]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (lets the compiler use SGPRs)
+  const int lr = lane & 15, lg = lane >> 4;
+
+  const int G = gridDim.x, b = blockIdx.x;
+  const int q = G >> 3, r = G & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int tm = L % p.tiles_m;
+  const int t2 = L / p.tiles_m;
+  const int z = t2 % p.splits;
+  const int tn = t2 / p.splits;
+
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int kb = z * p.kchunk;
+  const int ke = min(p.K, kb + p.kchunk);
+  const int T = ke > kb ? (ke - kb + 31) / 32 : 0;   // k32 steps
+  const int nst = (T + SPS - 1) / SPS;               // x stages
+
+  // this lane's W rows (one per fragment) as byte offsets in the tile's descriptor, and its 8-element K group
+  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+  uint32_t woff[FN];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(g[e]))) * rbf(u[e]));
-          uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
-          *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-        }
-      } else if (m < p.M && n < p.N) {
-        if (epi == EPI_F32) {
-          float* dst = reinterpret_cast<float*>(p.out) + z * p.part_stride + (int64_t)m * p.ldo + n;
-          *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-        } else {
-          uint32_t o[4];
-          if (epi == EPI_RESID) {
-            const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
-            const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
+  for (int f = 0; f < FN; ++f) woff[f] = (uint32_t)(((wave * FN + f) * 16 + lr) * p.ldw + kb + lg * 8) * 2u;
+  const int klim = ke - kb - lg * 8;  // step t is in range for this lane iff t * 32 < klim
+
+  bf16x8 wr[D][FN];
+  auto wload = [&](int slot, int t) {
+    const bool kin = t * 32 < klim;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = f2bf(rv[e] + rbf(v[e]));
-          } else {
+    for (int f = 0; f < FN; ++f)
+      wr[slot][f] = __builtin_bit_cast(bf16x8, bload(rsW, kin ? woff[f] + (uint32_t)t * 64u : kOOB));
+  };
+
+  uint4 rx[CX];
+  auto xload = [&](int st) {
+    const int k0 = kb + st * BKX;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) o[e] = f2bf(v[e]);
-          }
-          uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
-          *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-        }
+    for (int i = 0; i < CX; ++i) {
+      const int c = tid + i * NT;
+      const int row = c / CPR, col = (c % CPR) * 8;
+      const bool ok = (X_CH % NT == 0 || c < X_CH) && k0 + col < ke;
+      rx[i] = bload(rsX, ok ? (uint32_t)(row * p.ldx + k0 + col) * 2u : kOOB);
+    }
+  };
+  auto xstore = [&](int buf) {
+    uint16_t* x = sX + buf * BM * LS;
+#pragma unroll
+    for (int i = 0; i < CX; ++i) {
+      const int c = tid + i * NT;
+      if (X_CH % NT == 0 || c < X_CH) *reinterpret_cast<uint4*>(x + (c / CPR) * LS + (c % CPR) * 8) = rx[i];
+    }
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Steps run in rounds of R = max(D, SPS) so that the ring slot (t % D) and the step within the x stage
+  // (t % SPS) are compile-time constants; the step count is padded to whole rounds with zero loads.
+  constexpr int R = D > SPS ? D : SPS;
+  const int nround = (nst * SPS + R - 1) / R;
+  const int nst_p = nround * (R / SPS);  // x stages including padding (their loads are out of range: zeros)
+  if (nround > 0) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) wload(d, d);
+    xload(0);
+    xstore(0);
+    lds_barrier();
+    if (nst_p > 1) xload(1);
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+#pragma unroll
+    for (int j = 0; j < R; ++j) {
+      const int t = rd * R + j;
+      const int s = rd * (R / SPS) + j / SPS;
+      const int jj = j % SPS;
+      const uint16_t* xs = sX + (s & 1) * BM * LS + lr * LS + lg * 8 + jj * 32;
+      bf16x8 xf[FM];
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) xf[fm] = *reinterpret_cast<const bf16x8*>(xs + fm * 16 * LS);
+#pragma unroll
+      for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+          acc[f][fm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(wr[j % D][f], xf[fm], acc[f][fm], 0, 0, 0);
+      wload(j % D, t + D);
+      if (jj == SPS - 1) {
+        if (s + 1 < nst_p) xstore((s & 1) ^ 1);
+        lds_barrier();
+        if (s + 2 < nst_p) xload(s + 2);
       }
+    }
+  }
+
+  // epilogue: lane holds acc[f][fm][e] = y[m][n + e]
+#pragma unroll
+  for (int f = 0; f < FN; ++f) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int n = n0 + (wave * FN + f) * 16 + lg * 4;
+      const int m = m0 + fm * 16 + lr;
+      store_tile(p, epi, z, m, n, lg, acc[f][fm]);
+    }
+  }
+}
+
+
+// ------------------------------------------------------------------------------------------------ LDS-DMA
+// Both operand tiles go global -> LDS directly (buffer_load ... lds): no staging registers, so an NS-stage ring
+// of K tiles (64 k each) can be in flight within the 160 KB LDS. Each stage is its own static LDS array, which
+// gives every array its own alias scope, so the compiler's wait-count pass does not drain the whole queue before
+// reading a stage; the waits are explicit (vmcnt = loads of the younger stages still allowed in flight).
+//
+// Fragment-major LDS layout: a stage holds 16-row x 8-element blocks (256 B: row-major 16 B per row), ordered
+// (16-row group, k chunk). One DMA instruction fills 4 consecutive blocks with 1 KiB in lane order, and the MFMA
+// operand read of one 16-row fragment for one k32 step is the same 1 KiB read linearly: conflict-free both ways.
+template <int WN, int WM, int FN, int FM, int NS>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_dma_kernel(const GemmParams p, const int epi) {
+  constexpr int NW = WN * WM;
+  constexpr int BN = WN * FN * 16, BM = WM * FM * 16;
+  constexpr int IW = BN / 8, IX = BM / 8;   // 1 KiB DMA instructions per stage for W / x
+  constexpr int IPW = (IW + IX) / NW;       // per wave per stage
+  static_assert((IW + IX) % NW == 0, "DMA instructions must split evenly over the waves");
+  static_assert(NS >= 2 && NS <= 4, "2..4 stages");
+  constexpr int STB = (BN + BM) * 128;      // bytes per stage
+  constexpr int ALLOW = (NS - 2) * IPW;     // DMA instructions of younger stages allowed in flight
+  static_assert(ALLOW < 64, "vmcnt range");
+  constexpr int WAIT = (ALLOW & 0xF) | ((ALLOW >> 4) << 14) | (0x7 << 4);  // vmcnt(ALLOW) lgkmcnt(0)
+
+  __shared__ __attribute__((aligned(1024))) uint8_t st0[STB];
+  __shared__ __attribute__((aligned(1024))) uint8_t st1[STB];
+  __shared__ __attribute__((aligned(1024))) uint8_t st2[NS > 2 ? STB : 16];
+  __shared__ __attribute__((aligned(1024))) uint8_t st3[NS > 3 ? STB : 16];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (lets the compiler use SGPRs)
+  const int wn = wave % WN, wm = wave / WN;
+
+  const int G = gridDim.x, b = blockIdx.x;
+  const int q = G >> 3, r = G & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int tm = L % p.tiles_m;
+  const int t2 = L / p.tiles_m;
+  const int z = t2 % p.splits;
+  const int tn = t2 / p.splits;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int kb = z * p.kchunk;
+  const int ke = min(p.K, kb + p.kchunk);
+  const int nst = ke > kb ? (ke - kb + 63) / 64 : 0;
+
+  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+
+  // per-lane byte offsets (without the stage's k0) of this wave's DMA instructions
+  uint32_t voff[IPW];
+  int kcol[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int j = wave + i * NW;  // instruction index within the stage (W first, then x)
+    const bool isw = j < IW;
+    const int jj = isw ? j : j - IW;
+    const int blk = jj * 4 + (lane >> 4);
+    const int row = (blk >> 3) * 16 + (lane & 15);
+    kcol[i] = (blk & 7) * 8;
+    voff[i] = (uint32_t)(row * (isw ? p.ldw : p.ldx) + kb + kcol[i]) * 2u;
+  }
+  auto issue = [&](uint8_t* dst, int st) {
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int j = wave + i * NW;
+      const bool isw = j < IW;
+      const int ldsoff = isw ? j * 1024 : BN * 128 + (j - IW) * 1024;
+      const bool ok = st * 64 + kcol[i] < ke - kb;
+      dma16(isw ? rsW : rsX, dst + ldsoff, ok ? voff[i] + (uint32_t)st * 128u : kOOB);
+    }
+  };
+
+  f32x4 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](const uint8_t* cur) {
+    const uint8_t* wb = cur + (wn * FN) * 2048 + lane * 16;
+    const uint8_t* xb = cur + BN * 128 + (wm * FM) * 2048 + lane * 16;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 a[FN], x[FM];
+#pragma unroll
+      for (int f = 0; f < FN; ++f) a[f] = *reinterpret_cast<const bf16x8*>(wb + f * 2048 + kk * 1024);
+#pragma unroll
+      for (int fm = 0; fm < FM; ++fm) x[fm] = *reinterpret_cast<const bf16x8*>(xb + fm * 2048 + kk * 1024);
+#pragma unroll
+      for (int f = 0; f < FN; ++f)
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+          acc[f][fm] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[f], x[fm], acc[f][fm], 0, 0, 0);
+    }
+  };
+  auto barrier = [&]() {
+    __builtin_amdgcn_s_waitcnt(WAIT);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+  };
+
+  // prologue: stages 0 .. NS-2 in flight (padded stages read zeros)
+  issue(st0, 0);
+  if (NS > 2) issue(st1, 1);
+  if (NS > 3) issue(st2, 2);
+  for (int s = 0; s < nst; s += NS) {
+    // stage s lives in st0, s+1 in st1, ...; the stage issued at step s+i goes to the array stage s+i-1 used
+    barrier();
+    if (NS == 2) issue(st1, s + 1); else if (NS == 3) issue(st2, s + 2); else issue(st3, s + 3);
+    compute(st0);
+    if (s + 1 < nst) {
+      barrier();
+      if (NS == 2) issue(st0, s + 2); else if (NS == 3) issue(st0, s + 3); else issue(st0, s + 4);
+      compute(st1);
+    }
+    if (NS > 2 && s + 2 < nst) {
+      barrier();
+      if (NS == 3) issue(st1, s + 4); else issue(st1, s + 5);
+      compute(st2);
+    }
+    if (NS > 3 && s + 3 < nst) {
+      barrier();
+      issue(st2, s + 6);
+      compute(st3);
+    }
+  }
+  // drain the padded loads still in flight before the workgroup's LDS is reused
+  __builtin_amdgcn_s_waitcnt(0x7 << 4);
+
+#pragma unroll
+  for (int f = 0; f < FN; ++f) {
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) {
+      const int n = n0 + (wn * FN + f) * 16 + (lane >> 4) * 4;
+      const int m = m0 + (wm * FM + fm) * 16 + (lane & 15);
+      store_tile(p, epi, z, m, n, lane >> 4, acc[f][fm]);
     }
   }
 }
@@ -184,7 +482,13 @@ struct TileEntry {
 };
 
 #define OJX_TILE(BN, BM, BK, WN, WM)                                                                         \
-  {{BN, BM, BK, WN, WM, 64 * WN * WM, 2 * (BN + BM) * (BK + 8) * 2}, gemm_nt_kernel<BN, BM, BK, WN, WM>}
+  {{BN, BM, BK, WN, WM, 64 * WN * WM, 2 * (BN + BM) * (BK + 8) * 2, 0}, gemm_nt_kernel<BN, BM, BK, WN, WM>}
+// LDS-DMA tiles: WN x WM waves of FN x FM fragments, NS stages of 64 k (static LDS)
+#define OJX_DMA(WN, WM, FN, FM, NS)                                                                          \
+  {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 0, 2}, gemm_dma_kernel<WN, WM, FN, FM, NS>}
+// W-direct tiles: BN = NW*FN*16 W rows, BM = FM*16 x rows, x stage BKX, W ring depth D (k32 steps)
+#define OJX_WD(FN, FM, NW, D, BKX)                                                                           \
+  {{NW * FN * 16, FM * 16, BKX, NW, 1, 64 * NW, 2 * (FM * 16) * (BKX + 8) * 2, 1}, gemm_wd_kernel<FN, FM, NW, D, BKX>}
 
 // Order is the tile id used by the plan table; append only (ids are stored in plan_table.inc).
 static const TileEntry kTiles[] = {
@@ -204,6 +508,38 @@ static const TileEntry kTiles[] = {
     OJX_TILE(256, 96, 64, 4, 2),    // 13
     OJX_TILE(128, 144, 64, 2, 3),   // 14 M = 288 = 2 x 144
     OJX_TILE(64, 16, 256, 4, 1),    // 15 skinny M, deeper K
+    OJX_WD(4, 1, 4, 8, 256),        // 16 W-direct 256 x 16
+    OJX_WD(4, 2, 4, 8, 256),        // 17 256 x 32
+    OJX_WD(4, 4, 4, 4, 128),        // 18 256 x 64
+    OJX_WD(4, 6, 4, 4, 128),        // 19 256 x 96
+    OJX_WD(4, 8, 4, 4, 128),        // 20 256 x 128
+    OJX_WD(2, 9, 4, 4, 128),        // 21 128 x 144
+    OJX_WD(4, 9, 4, 2, 64),         // 22 256 x 144
+    OJX_WD(2, 18, 4, 2, 64),        // 23 128 x 288
+    OJX_WD(2, 8, 4, 4, 128),        // 24 128 x 128
+    OJX_WD(2, 4, 4, 8, 256),        // 25 128 x 64
+    OJX_WD(2, 1, 4, 8, 256),        // 26 128 x 16
+    OJX_WD(4, 3, 4, 4, 128),        // 27 256 x 48
+    OJX_WD(2, 18, 4, 8, 64),        // 28 128 x 288, deep W ring
+    OJX_WD(2, 18, 4, 12, 64),       // 29
+    OJX_WD(4, 9, 4, 8, 64),         // 30 256 x 144
+    OJX_WD(2, 9, 4, 16, 64),        // 31 128 x 144
+    OJX_WD(4, 6, 4, 8, 64),         // 32 256 x 96
+    OJX_WD(4, 4, 4, 8, 64),         // 33 256 x 64
+    OJX_WD(2, 4, 4, 16, 64),        // 34 128 x 64
+    OJX_WD(4, 1, 4, 16, 64),        // 35 256 x 16
+    OJX_WD(2, 2, 4, 16, 64),        // 36 128 x 32
+    OJX_DMA(2, 2, 4, 9, 3),         // 37 128 x 288
+    OJX_DMA(2, 2, 4, 4, 4),         // 38 128 x 128
+    OJX_DMA(2, 2, 6, 8, 2),         // 39 192 x 256
+    OJX_DMA(2, 2, 4, 8, 3),         // 40 128 x 256
+    OJX_DMA(2, 2, 8, 4, 3),         // 41 256 x 128
+    OJX_DMA(2, 2, 4, 6, 3),         // 42 128 x 192
+    OJX_DMA(2, 2, 2, 9, 3),         // 43 64 x 288
+    OJX_DMA(2, 2, 4, 2, 4),         // 44 128 x 64
+    OJX_DMA(2, 2, 4, 1, 4),         // 45 128 x 32
+    OJX_DMA(2, 2, 2, 1, 4),         // 46 64 x 32
+    OJX_DMA(2, 2, 4, 9, 2),         // 47 128 x 288, 2 stages
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];
@@ -218,6 +554,10 @@ const TileInfo* tile_info(int tile) {
 static hipError_t set_attr(int tile) {
   if (g_attr_set[tile]) return hipSuccess;
   const TileEntry& e = kTiles[tile];
+  if (e.info.lds_bytes == 0) {  // static LDS only
+    g_attr_set[tile] = true;
+    return hipSuccess;
+  }
   hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(e.fn),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, e.info.lds_bytes);
   if (err == hipSuccess) g_attr_set[tile] = true;

@@ -49,6 +49,7 @@ struct TileInfo {
   int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M
   int threads;
   int lds_bytes;
+  int family;  // 0: both operands through LDS; 1: W streamed straight into registers, x through LDS
 };
 
 // Tile registry (gemm.hip)
