@@ -40,10 +40,17 @@ enum {
   OJX_KIND_RESIDUAL = 2   /* out / o_proj / down projection with residual add (+ RMSNorm) */
 };
 
-/* One kernel configuration: a tile shape from the tile registry and a split-K count. */
+/* One kernel configuration: a tile shape from the tile registry and a split-K count. Optionally the last
+ * tail_rows rows of W (outputs N - tail_rows .. N - 1) run as a second launch with their own tile and split: when
+ * N / BN tiles leave a few tiles over a whole number of rounds on the 256 CUs, a finer tile for the remainder
+ * replaces a second, mostly idle round. tail_rows = 0 (the zero-initialised default) means no tail; tails apply
+ * to ojx_gemm_bf16 and ojx_gemm_silu_mul (tail_rows a multiple of 8 there). */
 typedef struct {
   int32_t tile;
   int32_t splitk;
+  int32_t tail_tile;
+  int32_t tail_splitk;
+  int32_t tail_rows;
 } ojx_cfg;
 
 const char* ojx_last_error(void);
@@ -52,9 +59,12 @@ const char* ojx_version(void);
 /* Sets kernel attributes on the current device. Optional: every launch does it on first use. */
 int ojx_init(void);
 
-/* Tile registry: info6 = {BN (W rows), BM (x rows), BK, waves along N, waves along M, threads}. */
+/* Tile registry: info7 = {BN (W rows), BM (x rows), BK, waves along N, waves along M, threads, family}.
+ * Family: 0 both operands via LDS, 1 W streamed to registers, 2 LDS DMA (all 16x16x32 MFMA); 3 W streamed to
+ * registers on 32x32x16 MFMA, 4 the same with x copied to LDS by DMA. Tiles of one MFMA shape sum K in the same order, so without split-K they give
+ * bit-identical results; across MFMA shapes results agree to fp32 rounding. */
 int ojx_num_tiles(void);
-int ojx_tile_info(int32_t tile, int32_t* info6);
+int ojx_tile_info(int32_t tile, int32_t* info7);
 
 /* Plan lookup for a shape: a static table measured offline on MI355X, with a heuristic for shapes not in it.
  * Never times anything, so it is safe during graph capture.

@@ -18,7 +18,12 @@ _f32 = ctypes.c_float
 
 
 class OjxCfg(ctypes.Structure):
-    _fields_ = [("tile", ctypes.c_int32), ("splitk", ctypes.c_int32)]
+    _fields_ = [("tile", ctypes.c_int32), ("splitk", ctypes.c_int32), ("tail_tile", ctypes.c_int32),
+                ("tail_splitk", ctypes.c_int32), ("tail_rows", ctypes.c_int32)]
+
+    def __repr__(self):
+        t = f", tail {self.tail_rows} rows: tile {self.tail_tile} S {self.tail_splitk}" if self.tail_rows else ""
+        return f"OjxCfg(tile {self.tile}, S {self.splitk}{t})"
 
 
 _cfgp = ctypes.POINTER(OjxCfg)
@@ -74,8 +79,8 @@ def check(rc: int) -> None:
         raise RuntimeError(f"ojx error {rc}: {lib().ojx_last_error().decode()}")
 
 
-def cfg(tile: int, splitk: int) -> OjxCfg:
-    return OjxCfg(tile, splitk)
+def cfg(tile: int, splitk: int, tail_tile: int = 0, tail_splitk: int = 1, tail_rows: int = 0) -> OjxCfg:
+    return OjxCfg(tile, splitk, tail_tile, tail_splitk, tail_rows)
 
 
 def plan(M: int, N: int, K: int, kind: int = KIND_PLAIN) -> OjxCfg:
@@ -85,9 +90,9 @@ def plan(M: int, N: int, K: int, kind: int = KIND_PLAIN) -> OjxCfg:
 
 
 def tile_info(tile: int):
-    info = (_i32 * 6)()
+    info = (_i32 * 7)()
     check(lib().ojx_tile_info(tile, info))
-    return dict(zip(("bn", "bm", "bk", "wn", "wm", "threads"), list(info)))
+    return dict(zip(("bn", "bm", "bk", "wn", "wm", "threads", "family"), list(info)))
 
 
 def candidates(M: int, N: int, K: int, kind: int = KIND_PLAIN):

@@ -32,7 +32,7 @@ inline int64_t kchunk_for(int64_t K, int64_t S) { return cdiv(cdiv(K, S), 8) * 8
 
 struct PlanEntry {
   int64_t M, N, K;
-  int32_t kind, tile, splitk;
+  int32_t kind, tile, splitk, tail_tile, tail_splitk, tail_rows;
 };
 
 // Measured on MI355X by the offline sweep (tuning script in the package); shapes not listed use heuristic_plan.
@@ -43,17 +43,46 @@ const PlanEntry kPlan[] = {
 constexpr int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
 constexpr int kMaxSplit = 16;
 
+bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
+  if (tile < 0 || tile >= ojx::num_tiles()) return false;
+  if (splitk < 1 || splitk > kMaxSplit) return false;
+  const int64_t ch = kchunk_for(K, splitk);
+  return (splitk - 1) * ch < K;  // every split owns a non-empty K range
+}
+
 bool cfg_fits(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
-  (void)M; (void)N;
-  if (c.tile < 0 || c.tile >= ojx::num_tiles()) return false;
-  if (c.splitk < 1 || c.splitk > kMaxSplit) return false;
-  const int64_t ch = kchunk_for(K, c.splitk);
-  return (c.splitk - 1) * ch < K;  // every split owns a non-empty K range
+  (void)M;
+  if (!part_fits(K, c.tile, c.splitk)) return false;
+  if (c.tail_rows == 0) return true;
+  return c.tail_rows > 0 && c.tail_rows < N && c.tail_rows % 8 == 0 && part_fits(K, c.tail_tile, c.tail_splitk);
+}
+
+// The launches of a configuration: rows [0, N - tail_rows) with (tile, splitk), then the tail.
+struct Part {
+  ojx_cfg c;     // tile and split of this launch (no tail)
+  int64_t n0, n; // W rows (output columns) it covers
+  int64_t ws;    // byte offset of its split-K partials in the workspace
+};
+int split_parts(const ojx_cfg& c, int64_t M, int64_t N, Part out[2]) {
+  const int64_t nt = c.tail_rows;
+  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, 0};
+  if (nt == 0) return 1;
+  const int64_t ws0 = c.splitk > 1 ? (int64_t)c.splitk * M * (N - nt) * 4 : 0;
+  out[1] = Part{ojx_cfg{c.tail_tile, c.tail_splitk, 0, 1, 0}, N - nt, nt, ws0};
+  return 2;
+}
+int64_t workspace_for(const ojx_cfg& c, int64_t M, int64_t N) {
+  Part parts[2];
+  const int np = split_parts(c, M, N, parts);
+  int64_t total = 0;
+  for (int i = 0; i < np; ++i)
+    if (parts[i].c.splitk > 1) total += (int64_t)parts[i].c.splitk * M * parts[i].n * 4;
+  return total;
 }
 
 ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
   (void)kind;
-  ojx_cfg c;
+  ojx_cfg c{};
   if (M <= 16) c.tile = 0;
   else if (M <= 32) c.tile = 2;
   else if (M <= 64) c.tile = 4;
@@ -71,8 +100,9 @@ ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
 int resolve(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg, ojx_cfg* out) {
   if (cfg != nullptr) {
     if (!cfg_fits(M, N, K, *cfg))
-      return fail(OJX_ERR_CONFIG, "config (tile %d, splitk %d) invalid for M=%lld N=%lld K=%lld", cfg->tile,
-                  cfg->splitk, (long long)M, (long long)N, (long long)K);
+      return fail(OJX_ERR_CONFIG, "config (tile %d, splitk %d, tail %d/%d/%d) invalid for M=%lld N=%lld K=%lld",
+                  cfg->tile, cfg->splitk, cfg->tail_tile, cfg->tail_splitk, cfg->tail_rows, (long long)M,
+                  (long long)N, (long long)K);
     *out = *cfg;
     return OJX_OK;
   }
@@ -156,11 +186,12 @@ int ojx_init(void) { return hip_check(ojx::init_tiles(), "kernel attribute setup
 
 int ojx_num_tiles(void) { return ojx::num_tiles(); }
 
-int ojx_tile_info(int32_t tile, int32_t* info6) {
+int ojx_tile_info(int32_t tile, int32_t* info7) {
   const ojx::TileInfo* t = ojx::tile_info(tile);
   if (t == nullptr) return fail(OJX_ERR_CONFIG, "tile %d out of range [0, %d)", tile, ojx::num_tiles());
-  if (info6 == nullptr) return fail(OJX_ERR_ARG, "null info");
-  info6[0] = t->bn; info6[1] = t->bm; info6[2] = t->bk; info6[3] = t->wn; info6[4] = t->wm; info6[5] = t->threads;
+  if (info7 == nullptr) return fail(OJX_ERR_ARG, "null info");
+  info7[0] = t->bn; info7[1] = t->bm; info7[2] = t->bk; info7[3] = t->wn; info7[4] = t->wm; info7[5] = t->threads;
+  info7[6] = t->family;
   return OJX_OK;
 }
 
@@ -169,12 +200,13 @@ int ojx_plan(int64_t M, int64_t N, int64_t K, int32_t kind, ojx_cfg* out) {
   if (kind < OJX_KIND_PLAIN || kind > OJX_KIND_RESIDUAL) return fail(OJX_ERR_ARG, "unknown kind %d", kind);
   for (const PlanEntry& e : kPlan) {
     if (e.M == M && e.N == N && e.K == K && e.kind == kind) {
-      ojx_cfg c{e.tile, e.splitk};
+      ojx_cfg c{e.tile, e.splitk, e.tail_tile, e.tail_splitk, e.tail_rows};
+      if (c.tail_splitk == 0) c.tail_splitk = 1;
       if (cfg_fits(M, N, K, c)) { *out = c; return OJX_OK; }
     }
   }
   *out = heuristic_plan(M, N, K, kind);
-  if (!cfg_fits(M, N, K, *out)) *out = ojx_cfg{out->tile, 1};
+  if (!cfg_fits(M, N, K, *out)) *out = ojx_cfg{out->tile, 1, 0, 1, 0};
   return OJX_OK;
 }
 
@@ -191,7 +223,7 @@ int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind) {
   (void)kind;
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
-    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s}) ? 1 : 0;
+    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}) ? 1 : 0;
   return n;
 }
 
@@ -201,17 +233,17 @@ int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, oj
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
     for (int s : kSplits)
-      if (candidate_ok(M, N, K, ojx_cfg{t, s})) {
-        if (n == idx) { *out = ojx_cfg{t, s}; return OJX_OK; }
+      if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0})) {
+        if (n == idx) { *out = ojx_cfg{t, s, 0, 1, 0}; return OJX_OK; }
         ++n;
       }
   return fail(OJX_ERR_CONFIG, "candidate index %d out of range [0, %d)", idx, n);
 }
 
 int64_t ojx_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg) {
-  ojx_cfg c;
+  ojx_cfg c{};
   if (resolve(M, N, K, kind, cfg, &c) != OJX_OK) return -1;
-  return c.splitk > 1 ? (int64_t)c.splitk * M * N * 4 : 0;
+  return workspace_for(c, M, N);
 }
 
 int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
@@ -222,15 +254,26 @@ int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, i
   OJX_TRY(check_operands(x, w, ldx, ldw, K));
   if (y == nullptr || !aligned(y, 8) || ldy < N || ldy % 4 != 0)
     return fail(OJX_ERR_ARG, "y must be 8-byte aligned with row stride >= N and a multiple of 4");
-  ojx_cfg c;
+  ojx_cfg c{};
   OJX_TRY(resolve(M, N, K, OJX_KIND_PLAIN, cfg, &c));
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N)));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (c.splitk == 1) return gemm(c, ojx::EPI_BF16, x, ldx, w, ldw, y, ldy, nullptr, 0, M, N, K, st);
-  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
-  float* parts = static_cast<float*>(workspace);
-  OJX_TRY(gemm(c, ojx::EPI_F32, x, ldx, w, ldw, parts, N, nullptr, 0, M, N, K, st));
-  return hip_check(ojx::launch_reduce_bf16(parts, c.splitk, M * N, static_cast<uint16_t*>(y), ldy, (int)M, (int)N,
-                                           st), "reduce launch");
+  Part parts[2];
+  const int np = split_parts(c, M, N, parts);
+  for (int i = 0; i < np; ++i) {
+    const Part& q = parts[i];
+    const void* wq = static_cast<const uint16_t*>(w) + q.n0 * ldw;
+    uint16_t* yq = static_cast<uint16_t*>(y) + q.n0;
+    if (q.c.splitk == 1) {
+      OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st));
+      continue;
+    }
+    float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
+    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, ldx, wq, ldw, pp, q.n, nullptr, 0, M, q.n, K, st));
+    OJX_TRY(hip_check(ojx::launch_reduce_bf16(pp, q.c.splitk, M * q.n, yq, ldy, (int)M, (int)q.n, st),
+                      "reduce launch"));
+  }
+  return OJX_OK;
 }
 
 int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, int64_t N, int64_t K, int64_t ldx,
@@ -239,7 +282,7 @@ int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, i
   if (M == 0) return OJX_OK;
   OJX_TRY(check_operands(x, w, ldx, ldw, K));
   if (parts == nullptr || !aligned(parts, 16)) return fail(OJX_ERR_ARG, "parts must be 16-byte aligned");
-  ojx_cfg c;
+  ojx_cfg c{};
   if (tile < 0) OJX_TRY(ojx_plan(M, N, K, OJX_KIND_RESIDUAL, &c));
   else c.tile = tile;
   c.splitk = S;
@@ -256,15 +299,26 @@ int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t
   if (M == 0) return OJX_OK;
   OJX_TRY(check_operands(x, w_gu_packed, K, K, K));
   if (out == nullptr || !aligned(out, 8)) return fail(OJX_ERR_ARG, "out must be 8-byte aligned");
-  ojx_cfg c;
+  ojx_cfg c{};
   OJX_TRY(resolve(M, N, K, OJX_KIND_SILU_MUL, cfg, &c));
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N)));
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (c.splitk == 1) return gemm(c, ojx::EPI_SILU, x, K, w_gu_packed, K, out, I, nullptr, 0, M, N, K, st);
-  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
-  float* parts = static_cast<float*>(workspace);
-  OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w_gu_packed, K, parts, N, nullptr, 0, M, N, K, st));
-  return hip_check(ojx::launch_reduce_silu(parts, c.splitk, M * N, static_cast<uint16_t*>(out), I, (int)M, (int)N,
-                                           st), "reduce launch");
+  Part parts[2];
+  const int np = split_parts(c, M, N, parts);
+  for (int i = 0; i < np; ++i) {
+    const Part& q = parts[i];
+    const void* wq = static_cast<const uint16_t*>(w_gu_packed) + q.n0 * K;
+    uint16_t* oq = static_cast<uint16_t*>(out) + q.n0 / 2;  // packed blocks of 8 rows give 4 output columns
+    if (q.c.splitk == 1) {
+      OJX_TRY(gemm(q.c, ojx::EPI_SILU, x, K, wq, K, oq, I, nullptr, 0, M, q.n, K, st));
+      continue;
+    }
+    float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
+    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, K, wq, K, pp, q.n, nullptr, 0, M, q.n, K, st));
+    OJX_TRY(hip_check(ojx::launch_reduce_silu(pp, q.c.splitk, M * q.n, oq, I, (int)M, (int)q.n, st),
+                      "reduce launch"));
+  }
+  return OJX_OK;
 }
 
 int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual, const float* w1,
@@ -282,8 +336,11 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
       return fail(OJX_ERR_ARG, "w1 and hn_out must be non-null and 16-byte aligned");
   }
   if (M == 0) return OJX_OK;
-  ojx_cfg c;
+  ojx_cfg c{};
   OJX_TRY(resolve(M, N, K, OJX_KIND_RESIDUAL, cfg, &c));
+  if (c.tail_rows != 0)
+    return fail(OJX_ERR_CONFIG, "tail configurations apply to the plain and SiLU.mul GEMMs only (the RMSNorm "
+                                "epilogue needs whole rows)");
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* h = static_cast<uint16_t*>(h_out);
   uint16_t* hn = static_cast<uint16_t*>(hn_out);

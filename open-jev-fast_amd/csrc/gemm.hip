@@ -20,6 +20,8 @@
 //     range, so a W tile is fetched from HBM into that XCD's L2 once.
 #include "ojx_internal.h"
 
+#include <type_traits>
+
 namespace ojx {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -36,6 +38,39 @@ __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor's range: the load returns zeros
 
+// The same descriptor as four dwords, for loads issued from inline assembly. The compiler's wait-count pass does
+// not track those loads; the kernel that uses them waits for them itself with an explicit s_waitcnt vmcnt(N),
+// where N counts the loads it issued after them. (Untracked loads only ever make the compiler's own waits on its
+// tracked loads stricter, never looser.)
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ u32x4 make_rsrc4(const void* base, int64_t bytes) {
+  const int32_t n = bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  u32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane((uint32_t)n);
+  r[3] = 0x00020000u;
+  return r;
+}
+__device__ __forceinline__ u32x4 bload_asm(const u32x4& r, uint32_t off) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(r) : "memory");
+  return v;
+}
+// Same load into accumulation registers (AGPRs): used for data that only goes on to LDS, so the compiler never has
+// a reason to copy or spill it before the explicit wait (it cannot tell that the load is still in flight).
+__device__ __forceinline__ u32x4 bload_asm_agpr(const u32x4& r, uint32_t off) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=a"(v) : "v"(off), "s"(r) : "memory");
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // 16-byte global -> LDS DMA: lane i of the wave writes lds + 16 i. (Kept out of the kernel templates: written
 // inline there, the address-space cast stops the host pass from emitting the kernels' launch stubs.)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
@@ -51,42 +86,47 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 
-// Epilogue of one 16x16 accumulator fragment: lane holds v[e] = y[m][n + e] (n a multiple of 4).
+// Epilogue of 4 consecutive outputs y[m][n .. n+3] (n a multiple of 4) held by one lane. For the fused SiLU.mul,
+// `u` is the partner lane's values: packed W_gu rows come in blocks of 8 (4 gate rows, then the 4 up rows of the
+// same columns), so a lane holding gate columns (`gate` true) finds its up columns in the partner lane.
+__device__ __forceinline__ void store4(const GemmParams& p, const int epi, const int z, const int m, const int n,
+                                       const bool gate, const f32x4 v, const f32x4 u) {
+  if (m >= p.M || n >= p.N) return;
+  if (epi == EPI_SILU) {
+    if (!gate) return;
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(v[e]))) * rbf(u[e]));
+    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
+    *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+  } else if (epi == EPI_F32) {
+    float* dst = reinterpret_cast<float*>(p.out) + z * p.part_stride + (int64_t)m * p.ldo + n;
+    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    uint32_t o[4];
+    if (epi == EPI_RESID) {
+      const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
+      const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f2bf(rv[e] + rbf(v[e]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = f2bf(v[e]);
+    }
+    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
+    *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+  }
+}
+
+__device__ __forceinline__ f32x4 shfl4(const f32x4 v, int mask) {
+  return f32x4{__shfl_xor(v[0], mask), __shfl_xor(v[1], mask), __shfl_xor(v[2], mask), __shfl_xor(v[3], mask)};
+}
+
+// Epilogue of one 16x16 accumulator fragment: lane holds v[e] = y[m][n + e]; lane group lg = lane / 16.
 __device__ __forceinline__ void store_tile(const GemmParams& p, const int epi, const int z, const int m, const int n,
                                            const int lg, const f32x4 v) {
-  if (epi == EPI_SILU) {
-    // Packed W_gu rows come in blocks of 8: 4 gate rows then the 4 up rows of the same columns, so lane
-    // group lg (even) holds gate columns and lane group lg+1 the matching up columns.
-    const float u0 = __shfl_xor(v[0], 16), u1 = __shfl_xor(v[1], 16);
-    const float u2 = __shfl_xor(v[2], 16), u3 = __shfl_xor(v[3], 16);
-    if ((lg & 1) == 0 && m < p.M && n < p.N) {
-      const float g[4] = {v[0], v[1], v[2], v[3]};
-      const float u[4] = {u0, u1, u2, u3};
-      uint32_t o[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(g[e]))) * rbf(u[e]));
-      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
-      *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-    }
-  } else if (m < p.M && n < p.N) {
-    if (epi == EPI_F32) {
-      float* dst = reinterpret_cast<float*>(p.out) + z * p.part_stride + (int64_t)m * p.ldo + n;
-      *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-    } else {
-      uint32_t o[4];
-      if (epi == EPI_RESID) {
-        const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
-        const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = f2bf(rv[e] + rbf(v[e]));
-      } else {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = f2bf(v[e]);
-      }
-      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
-      *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-    }
-  }
+  const f32x4 u = epi == EPI_SILU ? shfl4(v, 16) : v;  // all lanes take part in the exchange
+  store4(p, epi, z, m, n, (lg & 1) == 0, v, u);
 }
 
 template <int BN, int BM, int BK, int WN, int WM>
@@ -334,6 +374,373 @@ __global__ void __launch_bounds__(64 * NW) gemm_wd_kernel(const GemmParams p, co
 }
 
 
+
+// ------------------------------------------------------------------------------------------------ W-direct 32x32
+// v_mfma_f32_32x32x16_bf16 version of the weight-streaming design: each wave owns FN 32-row slabs of W, streamed
+// from HBM into operand registers through a ring of DG load groups, and multiplies them against FM 32-row x
+// fragments of the workgroup's x tile, which sits in LDS in stages of 64 k. WN x WM waves: waves with the same wn
+// stream the same W rows (the second request hits in L1/L2) and split the x tile (WM * FM fragments, all of M when
+// it fits), so W is fetched from HBM once per x tile and the LDS traffic is one 1 KiB x fragment per FN MFMAs.
+//
+// K order: the 16-k steps are taken in groups of G = 4. Within group u, lane group g = lane / 32 uses the
+// 8-element k chunks 8u + 4g + s for steps s = 0..3, so each lane reads 4 consecutive chunks (64 B) of its W row
+// in one go and a row's 128 B line is read whole by its two lanes. x fragments are read from LDS with the same
+// chunk mapping, so every product pairs matching k.
+//
+// Output layout of a 32x32 fragment: lane l holds rows (W) n = 8 r + 4 (l / 32) + e, r = 0..3, e = 0..3, of
+// column (x row) m = l % 32. A packed gate/up block of 8 rows therefore splits between lanes l and l ^ 32.
+template <int FN, int FM, int WN, int WM, int DG>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_w32_kernel(const GemmParams p, const int epi) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  constexpr int G = 4;                      // k16 steps per W load group and per x stage (64 k)
+  constexpr int NT = 64 * WN * WM;
+  constexpr int BN = WN * FN * 32, BM = WM * FM * 32;
+  constexpr int LS = 64 + 8;                // padded LDS row of one x stage (bf16)
+  constexpr int X_CH = BM * 8;              // 16-byte chunks per x stage
+  constexpr int CX = (X_CH + NT - 1) / NT;
+  constexpr int LPS = CX + FN * G;          // global loads each stage issues (x stage s + 2, W refill)
+  static_assert(DG >= 2 && DG % 2 == 0, "even ring depth: x register sets alternate with the stage parity");
+  static_assert((DG - 1) * LPS < 64 && FN * G + LPS < 64, "wait counts must fit vmcnt");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* sX = smem;  // [2][BM][LS]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wn = wave % WN, wm = wave / WN;  // W slab group, x fragment group of this wave
+
+  const int Gd = gridDim.x, b = blockIdx.x;
+  const int q = Gd >> 3, r = Gd & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int tm = L % p.tiles_m;
+  const int t2 = L / p.tiles_m;
+  const int z = t2 % p.splits;
+  const int tn = t2 / p.splits;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int kb = z * p.kchunk;
+  const int ke = min(p.K, kb + p.kchunk);
+  const int nst = ke > kb ? (ke - kb + 63) / 64 : 0;  // stages of 64 k (= W load groups)
+
+  const u32x4 rsW = make_rsrc4(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const u32x4 rsX = make_rsrc4(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+  uint32_t woff[FN];
+#pragma unroll
+  for (int f = 0; f < FN; ++f) woff[f] = (uint32_t)(((wn * FN + f) * 32 + lr) * p.ldw + kb + lh * 32) * 2u;
+  const int klim = ke - kb - lh * 32;  // chunk c of group u is in range for this lane iff u*64 + 8c < klim
+
+  // All global loads of the main loop are issued from inline assembly and waited for explicitly (see bload_asm):
+  // every stage issues the same loads in the same order (past the end they are out of range and read zeros), so
+  // each wait count below is exact.
+  u32x4 wr[DG][FN][G];
+  auto wload = [&](int slot, int u) {
+#pragma unroll
+    for (int f = 0; f < FN; ++f)
+#pragma unroll
+      for (int c = 0; c < G; ++c) {
+        const bool ok = u * 64 + c * 8 < klim;
+        wr[slot][f][c] = bload_asm(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
+      }
+  };
+  u32x4 rx[2][CX];
+  auto xload = [&](int set, int st) {
+    const int k0 = kb + st * 64;
+#pragma unroll
+    for (int i = 0; i < CX; ++i) {
+      const int c = tid + i * NT;
+      const int row = c >> 3, col = (c & 7) * 8;
+      const bool ok = (X_CH % NT == 0 || c < X_CH) && k0 + col < ke;
+      rx[set][i] = bload_asm_agpr(rsX, ok ? (uint32_t)(row * p.ldx + k0 + col) * 2u : kOOB);
+    }
+  };
+  // waits that also tie the awaited registers to the wait, so their consumers cannot move above it
+#define OJX_WAIT_W(N, slot)                                                                                    \
+  _Pragma("unroll") for (int f_ = 0; f_ < FN; ++f_)                                                         \
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(wr[slot][f_][0]), "+v"(wr[slot][f_][1]), "+v"(wr[slot][f_][2]),  \
+                 "+v"(wr[slot][f_][3]) : "n"(N) : "memory")
+#define OJX_WAIT_X(N, set)                                                                                     \
+  do {                                                                                                         \
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");                                                   \
+    _Pragma("unroll") for (int i_ = 0; i_ < CX; ++i_) asm volatile("" : "+a"(rx[set][i_]));                    \
+  } while (0)
+  auto xstore = [&](int set, int buf) {
+    const uint32_t x = (uint32_t)reinterpret_cast<uintptr_t>(sX + buf * BM * LS);
+#pragma unroll
+    for (int i = 0; i < CX; ++i) {
+      const int c = tid + i * NT;
+      if (X_CH % NT == 0 || c < X_CH) {
+        const uint32_t a = x + (uint32_t)(((c >> 3) * LS + (c & 7) * 8) * 2);
+        asm volatile("ds_write_b128 %0, %1" ::"v"(a), "a"(rx[set][i]) : "memory");
+      }
+    }
+  };
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // x fragment of step cs (0..3) of a stage held in LDS buffer buf: lane group lh reads chunk 4 lh + cs
+  auto xread = [&](bf16x8 (&xf)[FM], int buf, int cs) {
+    const uint16_t* xs = sX + buf * BM * LS + (wm * FM * 32 + lr) * LS + (lh * 4 + cs) * 8;
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) xf[fm] = *reinterpret_cast<const bf16x8*>(xs + fm * 32 * LS);
+  };
+
+  const int nround = (nst + DG - 1) / DG;  // stages run in rounds of DG: ring slots are compile-time
+  const int nst_p = nround * DG;           // padded stages read zeros
+  // Stage u of x lives in LDS buffer u & 1 and register set u & 1. It is loaded at the start of stage u - 3,
+  // written to LDS after the mid-stage barrier of stage u - 2 (into the buffer stage u - 2 has finished reading)
+  // and made visible by the barrier of stage u - 1, whose last step already prefetches its first fragments. The
+  // one barrier per stage thus sits between MFMA steps 2 and 3, with MFMA work queued on both sides of it.
+  // Every stage issues the same loads in the same order, x stage s + 3 then the W refill (group s + DG - 1 into the
+  // slot stage s - 1 consumed), and the prologue ends with the same pair, so each wait count is one constant: no
+  // stage-dependent branch around a wait. Loads complete in order for vmcnt, so the x wait is placed to let the
+  // latest W refill stay in flight.
+  bf16x8 xa[FM], xb[FM];
+  if (nround > 0) {
+    xload(0, 0);
+    xload(1, 1);
+#pragma unroll
+    for (int d = 0; d < DG - 2; ++d) wload(d, d);
+    OJX_WAIT_X(0, 0);
+    OJX_WAIT_X(0, 1);
+#pragma unroll
+    for (int d = 0; d < DG - 2; ++d) { OJX_WAIT_W(0, d); }
+    xstore(0, 0);
+    xstore(1, 1);
+    xload(0, 2);
+    wload(DG - 2, DG - 2);  // in the place of a stage's refill, after its x set
+    lds_barrier();
+    xread(xa, 0, 0);
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+#pragma unroll
+    for (int j = 0; j < DG; ++j) {
+      const int s = rd * DG + j;  // stage = W group
+      const int buf = s & 1;
+      xload((j + 1) & 1, s + 3);
+      wload((j + DG - 1) % DG, s + DG - 1);
+      // W group s, issued at stage s - DG + 1 (group DG - 2 at the end of the prologue) and followed by DG - 1
+      // whole stages (groups below DG - 2 were waited for in the prologue; the count then covers them trivially)
+      OJX_WAIT_W((DG - 1) * LPS, j);
+#pragma unroll
+      for (int cs = 0; cs < G; ++cs) {
+        bf16x8 (&cur)[FM] = (cs & 1) ? xb : xa;
+        bf16x8 (&nxt)[FM] = (cs & 1) ? xa : xb;
+        if (cs == G - 1) {
+          // x stage s + 2 (register set j & 1, loaded at the start of stage s - 1 or at the end of the prologue,
+          // followed by one refill and this stage's loads) goes into the buffer this stage has finished reading,
+          // once every wave is past its reads
+          OJX_WAIT_X(FN * G + LPS, j & 1);
+          lds_barrier();
+          xstore(j & 1, buf);
+          // first fragments of stage s + 1, written during stage s - 1 and visible since the barrier above
+          xread(nxt, buf ^ 1, 0);
+        } else {
+          // next step's fragments are read a whole step ahead of their MFMAs (the scheduling fences keep the
+          // compiler from sinking each read next to its use, which would expose the LDS latency on every MFMA)
+          xread(nxt, buf, cs + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int f = 0; f < FN; ++f)
+            acc[f][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wr[j][f][cs]), cur[fm],
+                                                                 acc[f][fm], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // padding loads still in flight
+
+#pragma unroll
+  for (int f = 0; f < FN; ++f)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const f32x4 v = {acc[f][fm][4 * rr], acc[f][fm][4 * rr + 1], acc[f][fm][4 * rr + 2], acc[f][fm][4 * rr + 3]};
+        const f32x4 u = epi == EPI_SILU ? shfl4(v, 32) : v;
+        const int n = n0 + (wn * FN + f) * 32 + 8 * rr + 4 * lh;
+        const int m = m0 + (wm * FM + fm) * 32 + lr;
+        store4(p, epi, z, m, n, lh == 0, v, u);
+      }
+#undef OJX_WAIT_W
+#undef OJX_WAIT_X
+}
+
+// ------------------------------------------------------------------------------------------------ W-direct 32x32, x by DMA
+// The 32x32 weight-streaming design of gemm_w32_kernel with x copied global -> LDS by the DMA path of buffer loads
+// (buffer_load_dwordx4 ... lds): no staging registers, no LDS store instructions. That leaves the register room for
+// FN = 2 slabs per wave (each x fragment read from LDS feeds FN MFMAs, and each x byte fetched serves BN W rows).
+//
+// x stage layout in LDS: BM rows of 64 k (128 B), unpadded. One DMA instruction fills 1 KiB = 8 rows, lane t
+// writing row t / 8 at 16-byte position q = t % 8; it fetches the row's chunk c = q ^ sw(row), sw(r) = (r / 2) % 8,
+// so a global row is still read as one whole 128 B line, and the fragment reads (32 rows, one chunk) spread over
+// all banks.
+__device__ __forceinline__ void dma16_asm(const u32x4& r, uint32_t lds_addr, uint32_t voff) {
+  asm volatile("buffer_load_dwordx4 %0, %1, 0 offen lds" ::"v"(voff), "s"(r), "{m0}"(lds_addr) : "memory");
+}
+
+template <int FN, int FM, int WN, int WM, int DG>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_w32d_kernel(const GemmParams p, const int epi) {
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  constexpr int G = 4;                       // k16 steps per W load group and per x stage (64 k)
+  constexpr int NWV = WN * WM;
+  constexpr int BN = WN * FN * 32, BM = WM * FM * 32;
+  constexpr int XB = BM * 128;               // bytes of one x stage
+  constexpr int CXD = BM / 8 / NWV;          // DMA instructions per wave per stage
+  static_assert(BM % (8 * NWV) == 0, "x stage rows must split evenly over the waves");
+  constexpr int LPS = FN * G + CXD;          // loads each stage issues (W refill, x stage s + 2)
+  static_assert(DG >= 2, "ring depth");
+  static_assert((DG - 1) * LPS < 64 && FN * G < 64, "wait counts must fit vmcnt");
+
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  const uint32_t sbase = (uint32_t)reinterpret_cast<uintptr_t>(smem);  // [2][BM][64] bf16, swizzled
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 31, lh = lane >> 5;
+  const int wn = wave % WN, wm = wave / WN;
+
+  const int Gd = gridDim.x, b = blockIdx.x;
+  const int q = Gd >> 3, r = Gd & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int tm = L % p.tiles_m;
+  const int t2 = L / p.tiles_m;
+  const int z = t2 % p.splits;
+  const int tn = t2 / p.splits;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int kb = z * p.kchunk;
+  const int ke = min(p.K, kb + p.kchunk);
+  const int nst = ke > kb ? (ke - kb + 63) / 64 : 0;
+
+  const u32x4 rsW = make_rsrc4(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const u32x4 rsX = make_rsrc4(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+  uint32_t woff[FN];
+#pragma unroll
+  for (int f = 0; f < FN; ++f) woff[f] = (uint32_t)(((wn * FN + f) * 32 + lr) * p.ldw + kb + lh * 32) * 2u;
+  const int klim = ke - kb - lh * 32;
+
+  // DMA source offsets: instruction i of this wave fills rows 8 (wave + i NWV) .. + 8 of the stage. With NWV even
+  // the swizzle sw(row) = (4 (wave + i NWV) + lane / 16) % 8 does not depend on i, so one chunk column and one
+  // offset serve all of the wave's instructions (instruction i adds 8 NWV rows).
+  static_assert(NWV % 2 == 0, "even wave count: one DMA column per lane");
+  const int xcol = ((lane & 7) ^ ((4 * wave + (lane >> 4)) & 7)) * 8;
+  const uint32_t xoff = (uint32_t)((8 * wave + (lane >> 3)) * p.ldx + kb + xcol) * 2u;
+  const uint32_t xstep = (uint32_t)(8 * NWV * p.ldx) * 2u;
+  u32x4 wr[DG][FN][G];
+  auto wload = [&](int slot, int u) {
+#pragma unroll
+    for (int f = 0; f < FN; ++f)
+#pragma unroll
+      for (int c = 0; c < G; ++c) {
+        const bool ok = u * 64 + c * 8 < klim;
+        wr[slot][f][c] = bload_asm(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
+      }
+  };
+  auto xdma = [&](int buf, int st) {
+    const bool ok = st * 64 + xcol < ke - kb;
+    const uint32_t o = xoff + (uint32_t)(st * 128);
+#pragma unroll
+    for (int i = 0; i < CXD; ++i)
+      dma16_asm(rsX, sbase + (uint32_t)(buf * XB + (wave + i * NWV) * 1024), ok ? o + i * xstep : kOOB);
+  };
+#define OJX_WAIT_W(N, slot)                                                                                    \
+  _Pragma("unroll") for (int f_ = 0; f_ < FN; ++f_)                                                         \
+    asm volatile("s_waitcnt vmcnt(%4)" : "+v"(wr[slot][f_][0]), "+v"(wr[slot][f_][1]), "+v"(wr[slot][f_][2]),  \
+                 "+v"(wr[slot][f_][3]) : "n"(N) : "memory")
+
+  f32x16 acc[FN][FM];
+#pragma unroll
+  for (int i = 0; i < FN; ++i)
+#pragma unroll
+    for (int j = 0; j < FM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // fragment reads: row r = (wm FM + fm) 32 + lr, chunk c = 4 lh + cs at position c ^ sw(r); sw depends on lr only
+  const int sw = (lr >> 1) & 7;
+  const uint16_t* xrow = smem + (wm * FM * 32 + lr) * 64;
+  auto xread = [&](bf16x8 (&xf)[FM], int buf, int cs) {
+    const uint16_t* xs = xrow + buf * (XB / 2) + (((lh * 4 + cs) ^ sw) * 8);
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm) xf[fm] = *reinterpret_cast<const bf16x8*>(xs + fm * 32 * 64);
+  };
+
+  const int nround = (nst + DG - 1) / DG;
+  // Schedule (stage s = W group s = x stage s, x stage u in LDS buffer u & 1): at the start of stage s the W slot
+  // stage s - 1 used is refilled with group s + DG - 1; between MFMA steps 2 and 3 the wave waits for its DMA of
+  // stage s + 1 (issued one stage earlier, followed only by this stage's refill), passes the barrier that makes all
+  // of stage s + 1 visible and frees buffer s & 1, then DMAs stage s + 2 into that buffer and prefetches the first
+  // fragments of stage s + 1.
+  bf16x8 xa[FM], xb[FM];
+  if (nround > 0) {
+    xdma(0, 0);
+    xdma(1, 1);
+#pragma unroll
+    for (int d = 0; d < DG - 1; ++d) wload(d, d);
+    wait_vmcnt<0>();
+#pragma unroll
+    for (int d = 0; d < DG - 1; ++d) { OJX_WAIT_W(0, d); }
+    lds_barrier();
+    xread(xa, 0, 0);
+  }
+  for (int rd = 0; rd < nround; ++rd) {
+#pragma unroll
+    for (int j = 0; j < DG; ++j) {
+      const int s = rd * DG + j;
+      const int buf = s & 1;
+      wload((j + DG - 1) % DG, s + DG - 1);
+      // group s: issued at the start of stage s - DG + 1, followed by DG - 1 whole stages of loads less that
+      // stage's own refill... counted exactly: that stage's DMA, DG - 2 full stages, this stage's refill
+      OJX_WAIT_W((DG - 1) * LPS, j);
+#pragma unroll
+      for (int cs = 0; cs < G; ++cs) {
+        bf16x8 (&cur)[FM] = (cs & 1) ? xb : xa;
+        bf16x8 (&nxt)[FM] = (cs & 1) ? xa : xb;
+        if (cs == G - 1) {
+          asm volatile("s_waitcnt vmcnt(%0)" ::"n"(FN * G) : "memory");
+          lds_barrier();
+          xdma(buf, s + 2);
+          xread(nxt, buf ^ 1, 0);
+        } else {
+          xread(nxt, buf, cs + 1);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+          for (int f = 0; f < FN; ++f)
+            acc[f][fm] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, wr[j][f][cs]), cur[fm],
+                                                                 acc[f][fm], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  }
+  wait_vmcnt<0>();  // padding loads still in flight
+  lds_barrier();    // and the last DMAs' writes, before the workgroup's LDS can be handed to another one
+
+#pragma unroll
+  for (int f = 0; f < FN; ++f)
+#pragma unroll
+    for (int fm = 0; fm < FM; ++fm)
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const f32x4 v = {acc[f][fm][4 * rr], acc[f][fm][4 * rr + 1], acc[f][fm][4 * rr + 2], acc[f][fm][4 * rr + 3]};
+        const f32x4 u = epi == EPI_SILU ? shfl4(v, 32) : v;
+        const int n = n0 + (wn * FN + f) * 32 + 8 * rr + 4 * lh;
+        const int m = m0 + (wm * FM + fm) * 32 + lr;
+        store4(p, epi, z, m, n, lh == 0, v, u);
+      }
+#undef OJX_WAIT_W
+}
+
 // ------------------------------------------------------------------------------------------------ LDS-DMA
 // Both operand tiles go global -> LDS directly (buffer_load ... lds): no staging registers, so an NS-stage ring
 // of K tiles (64 k each) can be in flight within the 160 KB LDS. Each stage is its own static LDS array, which
@@ -486,6 +893,13 @@ struct TileEntry {
 // LDS-DMA tiles: WN x WM waves of FN x FM fragments, NS stages of 64 k (static LDS)
 #define OJX_DMA(WN, WM, FN, FM, NS)                                                                          \
   {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 0, 2}, gemm_dma_kernel<WN, WM, FN, FM, NS>}
+// W-direct 32x32 tiles: BN = WN*FN*32 W rows, BM = WM*FM*32 x rows, W ring of DG groups of 64 k, x stages of 64 k
+#define OJX_W32D(FN, FM, WN, WM, DG)                                                                         \
+  {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 128, 4},                      \
+   gemm_w32d_kernel<FN, FM, WN, WM, DG>}
+#define OJX_W32(FN, FM, WN, WM, DG)                                                                          \
+  {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 72 * 2, 3},                   \
+   gemm_w32_kernel<FN, FM, WN, WM, DG>}
 // W-direct tiles: BN = NW*FN*16 W rows, BM = FM*16 x rows, x stage BKX, W ring depth D (k32 steps)
 #define OJX_WD(FN, FM, NW, D, BKX)                                                                           \
   {{NW * FN * 16, FM * 16, BKX, NW, 1, 64 * NW, 2 * (FM * 16) * (BKX + 8) * 2, 1}, gemm_wd_kernel<FN, FM, NW, D, BKX>}
@@ -540,6 +954,31 @@ static const TileEntry kTiles[] = {
     OJX_DMA(2, 2, 4, 1, 4),         // 45 128 x 32
     OJX_DMA(2, 2, 2, 1, 4),         // 46 64 x 32
     OJX_DMA(2, 2, 4, 9, 2),         // 47 128 x 288, 2 stages
+    OJX_W32(1, 9, 4, 1, 4),         // 48 128 x 288 (32x32 MFMA, all of M = 288 per tile)
+    OJX_W32(1, 9, 4, 1, 2),         // 49
+    OJX_W32(1, 4, 4, 1, 4),         // 50 128 x 128
+    OJX_W32(2, 4, 4, 1, 2),         // 51 256 x 128
+    OJX_W32(1, 2, 4, 1, 4),         // 52 128 x 64
+    OJX_W32(2, 2, 4, 1, 4),         // 53 256 x 64
+    OJX_W32(1, 1, 4, 1, 4),         // 54 128 x 32
+    OJX_W32(2, 1, 4, 1, 4),         // 55 256 x 32
+    OJX_W32(1, 6, 4, 1, 4),         // 56 128 x 192
+    OJX_W32(1, 8, 4, 1, 4),         // 57 128 x 256
+    OJX_W32(1, 3, 4, 1, 4),         // 58 128 x 96
+    OJX_W32(1, 5, 4, 1, 4),         // 59 128 x 160
+    OJX_W32(2, 5, 2, 2, 2),         // 60 128 x 320 (M = 288 + 1 padded fragment), x split over 2 waves
+    OJX_W32(2, 4, 2, 2, 4),         // 61 128 x 256
+    OJX_W32(2, 4, 2, 2, 2),         // 62 128 x 256
+    OJX_W32(2, 3, 2, 2, 2),         // 63 128 x 192
+    OJX_W32(2, 2, 2, 2, 4),         // 64 128 x 128
+    OJX_W32(2, 1, 2, 2, 4),         // 65 128 x 64
+    OJX_W32D(1, 9, 4, 1, 4),        // 66 128 x 288, x by DMA
+    OJX_W32D(2, 3, 4, 1, 2),        // 67 256 x 96
+    OJX_W32D(2, 8, 4, 1, 2),        // 68 256 x 256
+    OJX_W32D(2, 6, 4, 1, 2),        // 69 256 x 192
+    OJX_W32D(2, 4, 4, 1, 2),        // 70 256 x 128
+    OJX_W32D(2, 5, 2, 2, 2),        // 71 128 x 320
+    OJX_W32D(1, 9, 4, 1, 2),        // 72 128 x 288
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

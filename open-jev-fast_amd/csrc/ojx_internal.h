@@ -49,7 +49,8 @@ struct TileInfo {
   int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M
   int threads;
   int lds_bytes;
-  int family;  // 0: both operands through LDS; 1: W streamed straight into registers, x through LDS
+  int family;  // 0: both operands through LDS; 1: W streamed straight into registers, x through LDS; 2: LDS DMA;
+               // 3: 32x32 MFMA, W streamed, x staged through registers; 4: 32x32 MFMA, W streamed, x by DMA
 };
 
 // Tile registry (gemm.hip)

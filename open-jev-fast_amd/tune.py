@@ -49,6 +49,7 @@ def main():
     ap.add_argument("--tiles", default="", help="only these tile ids")
     ap.add_argument("--max-waves", type=float, default=16.0, help="skip candidates with more workgroups than this "
                     "many per CU")
+    ap.add_argument("--no-tails", action="store_true", help="simple (tile, split-K) candidates only")
     args = ap.parse_args()
     Ms = [int(m) for m in args.m.split(",")] if args.m else list(M_DEFAULT)
     names = args.shapes.split(",") if args.shapes else list(TUNE_SHAPES)
@@ -72,6 +73,16 @@ def main():
 
             results = []
             only = {int(t) for t in args.tiles.split(",")} if args.tiles else None
+
+            def timed(key):
+                try:
+                    cc = _lib.cfg(*key)
+                    t = perf.gpu_time([call(w, cc) for w in ws], iters=args.iters, reps=args.reps)
+                except RuntimeError as e:
+                    print(json.dumps({"shape": name, "M": M, "cfg": key, "error": str(e)}), flush=True)
+                    return
+                results.append((t, key))
+
             for c in _lib.candidates(M, N, K, kid):
                 if only is not None and c.tile not in only:
                     continue
@@ -79,20 +90,39 @@ def main():
                 wgs = -(-N // info["bn"]) * -(-M // info["bm"]) * c.splitk
                 if wgs > args.max_waves * 256:
                     continue
-                cc = _lib.cfg(c.tile, c.splitk)
-                try:
-                    t = perf.gpu_time([call(w, cc) for w in ws], iters=args.iters, reps=args.reps)
-                except RuntimeError as e:
-                    print(json.dumps({"shape": name, "M": M, "tile": c.tile, "splitk": c.splitk, "error": str(e)}),
-                          flush=True)
-                    continue
-                results.append((t, c.tile, c.splitk))
+                timed((c.tile, c.splitk, 0, 1, 0))
+            if kind != "residual" and not args.no_tails:
+                # tail configurations: the best simple tiles over whole rounds of 256 workgroups, the leftover
+                # rows with a finer tile
+                simple = sorted(results)
+                mains, seen = [], []
+                for t, key in simple:
+                    if len(seen) == 4:
+                        break
+                    if key[0] not in seen:
+                        seen.append(key[0])
+                        mains += [(key[0], 1), (key[0], 2)]
+                tails = [c for c in _lib.candidates(M, N, K, kid) if c.splitk <= 4 and (only is None or c.tile in only)]
+                for tile, S in mains:
+                    info = _lib.tile_info(tile)
+                    per_tile = -(-M // info["bm"]) * S
+                    tiles_n = -(-N // info["bn"])
+                    rounds = tiles_n * per_tile // 256
+                    n1 = (rounds * 256 // per_tile) * info["bn"]
+                    tr = N - n1
+                    if rounds == 0 or tr <= 0 or tr % 8 or tiles_n * per_tile % 256 == 0:
+                        continue
+                    for c in tails:
+                        ti = _lib.tile_info(c.tile)
+                        if -(-tr // ti["bn"]) * -(-M // ti["bm"]) * c.splitk > 512:
+                            continue
+                        timed((tile, S, c.tile, c.splitk, tr))
             results.sort()
             # accept the fastest candidate whose numerics pass
             ref = None
             best = None
-            for t, tile, S in results[:5]:
-                cc = _lib.cfg(tile, S)
+            for t, key in results[:5]:
+                cc = _lib.cfg(*key)
                 w = ws[0]
                 if kind == "plain":
                     out = ext.mm(x, w, cfg=cc).float()
@@ -109,27 +139,29 @@ def main():
                 d = (out - ref).abs()
                 ok = (d.max() / ref.abs().max() <= 1e-2) and (d.mean() <= 1e-3 * ref.pow(2).mean().sqrt())
                 if bool(ok):
-                    best = (t, tile, S)
+                    best = (t, key)
                     break
-                print(json.dumps({"shape": name, "M": M, "tile": tile, "splitk": S, "numerics": "FAIL"}), flush=True)
-            top = [{"us": round(t * 1e6, 2), "tile": tl, "splitk": s}
-                   for t, tl, s in (results if args.all else results[:6])]
+                print(json.dumps({"shape": name, "M": M, "cfg": key, "numerics": "FAIL"}), flush=True)
+            top = [{"us": round(t * 1e6, 2), "tile": k[0], "splitk": k[1], **({"tail": k[2:]} if k[4] else {})}
+                   for t, k in (results if args.all else results[:6])]
             if best is None:
                 print(json.dumps({"shape": name, "M": M, "error": "no valid candidate", "top": top}), flush=True)
                 continue
-            t, tile, S = best
+            t, key = best
             r = perf.roofline(M, N, K, kind, t)
-            print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "kind": kind, "tile": tile, "splitk": S,
-                              "us": round(t * 1e6, 2), "frac": round(r["frac"], 4), "tflops": round(r["tflops"], 1),
+            print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "kind": kind, "tile": key[0],
+                              "splitk": key[1], "tail": key[2:], "us": round(t * 1e6, 2),
+                              "frac": round(r["frac"], 4), "tflops": round(r["tflops"], 1),
                               "gbs": round(r["gbs"], 1), "top": top}), flush=True)
-            rows.append((M, N, K, kid, tile, S, t))
+            rows.append((M, N, K, kid, key, t))
         del ws
         torch.cuda.empty_cache()
     if args.out:
         with open(args.out, "w") as f:
-            f.write("// {M, N, K, kind, tile, splitk} measured by open-jev-fast_amd/tune.py on MI355X (us in comment)\n")
-            for M, N, K, kid, tile, S, t in rows:
-                f.write(f"{{{M}, {N}, {K}, {kid}, {tile}, {S}}},  // {t * 1e6:.1f} us\n")
+            f.write("// {M, N, K, kind, tile, splitk, tail_tile, tail_splitk, tail_rows} measured by "
+                    "open-jev-fast_amd/tune.py on MI355X (us in comment)\n")
+            for M, N, K, kid, key, t in rows:
+                f.write(f"{{{M}, {N}, {K}, {kid}, {', '.join(str(v) for v in key)}}},  // {t * 1e6:.1f} us\n")
 
 
 if __name__ == "__main__":

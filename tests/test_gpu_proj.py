@@ -53,14 +53,20 @@ def test_mm_planned_and_f64(pkg, ext, O, dev, M, N, K):
 
 
 def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
-    """Without split-K every tile sums K in the same order: outputs are bit-identical across tiles and runs."""
+    """Without split-K the tiles of one MFMA shape sum K in the same order: outputs are bit-identical across those
+    tiles and across runs (16x16x32 families 0-2; the 32x32x16 families 3-4 among themselves)."""
     M, N, K = 96, 512, 1024
     x, w = O.seeded_inputs(M, N, K, seed=3)
     xd, wd = x.to(dev), w.to(dev)
     _say("case tile invariance")
-    base = ext.mm(xd, wd, cfg=(0, 1))
+    base = {}
     for t in _tiles(pkg):
-        assert torch.equal(ext.mm(xd, wd, cfg=(t, 1)), base), f"tile {t}"
+        shape = 32 if pkg._lib.tile_info(t)["family"] in (3, 4) else 16
+        y = ext.mm(xd, wd, cfg=(t, 1))
+        if shape not in base:
+            base[shape] = y
+        assert torch.equal(y, base[shape]), f"tile {t}"
+    assert len(base) == 2
     for S in (2, 4):
         a = ext.mm(xd, wd, cfg=(6, S))
         assert torch.equal(a, ext.mm(xd, wd, cfg=(6, S))), "split-K not deterministic"
@@ -93,6 +99,43 @@ def test_mm_strided_and_errors(pkg, ext, O, dev):
         ext.mm(x.to(dev).t(), w.to(dev))  # not contiguous
     y = ext.mm(torch.empty(0, 64, dtype=torch.bfloat16, device=dev), w.to(dev))
     assert y.shape == (0, 64)
+
+
+# ----------------------------------------------------------------------------------------------- tail configs
+@pytest.mark.parametrize("M", [37, 288])
+def test_tail_configs(pkg, ext, O, dev, M):
+    """A configuration with a tail runs the last tail_rows W rows as a second launch with its own tile and split.
+    With S = 1 in both parts and tiles of one MFMA shape, the result is bit-identical to the single launch."""
+    N, K = 1000, 640
+    x, w = O.seeded_inputs(M, N, K, seed=M + 11)
+    ref = O.linear_bf16(x, w)
+    xd, wd = x.to(dev), w.to(dev)
+    for key in [(66, 1, 54, 1, 232), (14, 2, 0, 3, 488), (48, 1, 66, 2, 104), (6, 1, 6, 1, 8)]:
+        _say(f"case tail mm M={M} cfg={key}")
+        y = ext.mm(xd, wd, cfg=key)
+        _assert_tol(O, y, ref, f"cfg {key}")
+        if key[1] == 1 and key[3] == 1:
+            fam = lambda t: pkg._lib.tile_info(t)["family"] in (3, 4)  # noqa: E731
+            if fam(key[0]) == fam(key[2]):
+                assert torch.equal(y, ext.mm(xd, wd, cfg=(key[0], 1))), f"cfg {key} not bit-identical"
+    I = 264
+    g = torch.Generator().manual_seed(M)
+    wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    ref = O.gate_up_silu(x, wg, wu)
+    packed = ext.pack_gate_up(wg.to(dev), wu.to(dev))
+    for key in [(66, 1, 54, 1, 144), (14, 2, 49, 2, 16), (6, 1, 6, 1, 8)]:
+        _say(f"case tail silu M={M} cfg={key}")
+        out = ext.mm_silu_mul(xd, packed, cfg=key)
+        _assert_tol(O, out, ref, f"cfg {key}")
+        if key[1] == 1 and key[3] == 1:
+            assert torch.equal(out, ext.mm_silu_mul(xd, packed, cfg=(key[0], 1))), f"cfg {key}"
+    for bad in [(6, 1, 6, 1, 4), (6, 1, 6, 1, N), (6, 1, 999, 1, 8), (6, 1, 6, 0, 8)]:
+        with pytest.raises(RuntimeError):
+            ext.mm(xd, wd, cfg=bad)
+    h = torch.randn(M, N).bfloat16().to(dev)
+    with pytest.raises(RuntimeError):
+        ext.mm_residual_rmsnorm(h, xd, wd, torch.ones(N, device=dev), None, 1e-6, cfg=(6, 1, 6, 1, 8))
 
 
 # ----------------------------------------------------------------------------------------------- gate-up
