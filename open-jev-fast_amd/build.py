@@ -12,13 +12,14 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libojx.so")
-SOURCES = ["gemm.hip", "epilogue.hip", "api.hip"]
+SOURCES = ["gemm.hip", "gemm_sk.hip", "epilogue.hip", "api.hip"]
+OBJDIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 
 # -packed-fp32-ops off: hipcc would otherwise fuse float pairs into v_pk_{add,mul,fma}_f32, which this fleet
 # must not run. The host pass warns that it does not know the feature; that warning is expected.
-FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
+FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
          # the fragment epilogues must unroll completely, or the accumulator array is left in scratch memory
          "-mllvm", "-pragma-unroll-threshold=1000000",
@@ -26,16 +27,30 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", "-shared", f"--offload-arch={ARCH}",
 
 
 def build(verbose: bool = False) -> str:
-    """Compiles every source into libojx.so (always rebuilds). Returns the library path."""
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *FLAGS, *[os.path.join(CSRC, s) for s in SOURCES], "-o", tmp]
-    res = subprocess.run(cmd, capture_output=True, text=True)
+    """Compiles every source into libojx.so (always rebuilds; the translation units compile in parallel).
+    Returns the library path."""
+    os.makedirs(OBJDIR, exist_ok=True)
     noise = "is not a recognized feature for this target"
-    err = "\n".join(l for l in res.stderr.splitlines() if noise not in l)
+    jobs = []
+    for s in SOURCES:
+        obj = os.path.join(OBJDIR, s.replace(".hip", ".o"))
+        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, s), "-o", obj]
+        jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
+    errs = []
+    for cmd, obj, pr in jobs:
+        _, err = pr.communicate()
+        err = "\n".join(l for l in err.splitlines() if noise not in l)
+        if pr.returncode != 0:
+            errs.append(f"hipcc failed ({pr.returncode}):\n{' '.join(cmd)}\n{err}")
+        elif verbose and err.strip():
+            print(err, file=sys.stderr)
+    if errs:
+        raise RuntimeError("\n".join(errs))
+    tmp = LIB + ".tmp"
+    cmd = [HIPCC, "-shared", f"--offload-arch={ARCH}", *[o for _, o, _ in jobs], "-o", tmp]
+    res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
-        raise RuntimeError(f"hipcc failed ({res.returncode}):\n{' '.join(cmd)}\n{err}")
-    if verbose and err.strip():
-        print(err, file=sys.stderr)
+        raise RuntimeError(f"link failed ({res.returncode}):\n{' '.join(cmd)}\n{res.stderr}")
     os.replace(tmp, LIB)
     return LIB
 

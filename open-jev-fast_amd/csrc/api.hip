@@ -5,6 +5,8 @@
 
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
+#include <algorithm>
 #include <string>
 
 namespace {
@@ -43,9 +45,62 @@ const PlanEntry kPlan[] = {
 constexpr int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
 constexpr int kMaxSplit = 16;
 
+constexpr int kSkMaxPieces = 64;  // gemm_sk.hip: pieces one stream-K tile may be split into
+// Every workspace starts with this many bytes of stream-K arrival counters (one per remainder tile, fewer than the
+// grid): zero before the first call, left zero by every call. The launch data (partial tiles, split-K planes)
+// follows, so no layout ever writes over the counters.
+constexpr int64_t kCntBytes = 4096;
+constexpr int kMaxGrid = (int)(kCntBytes / 4);
+
+bool is_sk(int32_t tile) {
+  const ojx::TileInfo* t = ojx::tile_info(tile);
+  return t != nullptr && t->family == 5;
+}
+
+// Compute units of the current device (the persistent grid size), cached per device.
+int device_cus() {
+  static int cus[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return std::min(cus[dev], kMaxGrid);
+}
+
+// Work split of the persistent stream-K family: whole-tile waves of `grid` workgroups over the first dp tiles,
+// then the K iterations of the remaining R tiles shared by gs workgroups (at most S pieces per tile on average).
+struct SkPlan {
+  int grid, dp, gs;
+  bool partial;        // some tile is split over several workgroups: counters and partial slots are used
+  int64_t slot_bytes;  // 2 gs partial tiles of fp32
+};
+SkPlan sk_plan(const ojx::TileInfo* t, int64_t M, int64_t N, int64_t K, int32_t S) {
+  SkPlan sp{};
+  const int64_t tiles = cdiv(N, t->bn) * cdiv(M, t->bm);
+  const int64_t ipt = cdiv(K, 64);
+  const int64_t G = device_cus();
+  const int64_t dp = (tiles / G) * G, R = tiles - dp;
+  int64_t gs = 0;
+  if (R > 0) {
+    gs = std::min(std::min(G, R * (int64_t)S), R * ipt);
+    // keep every tile within kSkMaxPieces pieces: a tile spans at most (ipt - 1) / floor(T / gs) + 2 ranges
+    while (gs > R && (ipt - 1) / ((R * ipt) / gs) + 2 > kSkMaxPieces) --gs;
+  }
+  sp.dp = (int)dp;
+  sp.gs = (int)gs;
+  sp.grid = (int)(dp > 0 ? G : std::max<int64_t>(gs, 1));
+  sp.partial = gs > R;
+  sp.slot_bytes = gs > R ? 2 * gs * (int64_t)t->bn * t->bm * 4 : 0;
+  return sp;
+}
+
 bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
   if (tile < 0 || tile >= ojx::num_tiles()) return false;
   if (splitk < 1 || splitk > kMaxSplit) return false;
+  if (is_sk(tile)) return true;  // splitk is the stream-K spread there, not a K split
   const int64_t ch = kchunk_for(K, splitk);
   return (splitk - 1) * ch < K;  // every split owns a non-empty K range
 }
@@ -63,21 +118,28 @@ struct Part {
   int64_t n0, n; // W rows (output columns) it covers
   int64_t ws;    // byte offset of its split-K partials in the workspace
 };
-int split_parts(const ojx_cfg& c, int64_t M, int64_t N, Part out[2]) {
+// Workspace of one launch: the stream-K counters and partial slots, or the split-K fp32 planes.
+int64_t part_ws_bytes(const ojx_cfg& c, int64_t M, int64_t n, int64_t K) {
+  if (is_sk(c.tile)) {
+    const SkPlan sp = sk_plan(ojx::tile_info(c.tile), M, n, K, c.splitk);
+    return sp.slot_bytes;
+  }
+  return c.splitk > 1 ? cdiv((int64_t)c.splitk * M * n * 4, 256) * 256 : 0;
+}
+int split_parts(const ojx_cfg& c, int64_t M, int64_t N, int64_t K, Part out[2]) {
   const int64_t nt = c.tail_rows;
-  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, 0};
+  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, kCntBytes};
   if (nt == 0) return 1;
-  const int64_t ws0 = c.splitk > 1 ? (int64_t)c.splitk * M * (N - nt) * 4 : 0;
+  const int64_t ws0 = kCntBytes + part_ws_bytes(out[0].c, M, N - nt, K);
   out[1] = Part{ojx_cfg{c.tail_tile, c.tail_splitk, 0, 1, 0}, N - nt, nt, ws0};
   return 2;
 }
-int64_t workspace_for(const ojx_cfg& c, int64_t M, int64_t N) {
+int64_t workspace_for(const ojx_cfg& c, int64_t M, int64_t N, int64_t K) {
   Part parts[2];
-  const int np = split_parts(c, M, N, parts);
+  const int np = split_parts(c, M, N, K, parts);
   int64_t total = 0;
-  for (int i = 0; i < np; ++i)
-    if (parts[i].c.splitk > 1) total += (int64_t)parts[i].c.splitk * M * parts[i].n * 4;
-  return total;
+  for (int i = 0; i < np; ++i) total += part_ws_bytes(parts[i].c, M, parts[i].n, K);
+  return total > 0 ? kCntBytes + total : 0;
 }
 
 ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
@@ -121,7 +183,8 @@ int check_dims(int64_t M, int64_t N, int64_t K) {
 
 // One GEMM launch with the given tile / split count and epilogue.
 int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
-         const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st) {
+         const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st, void* ws = nullptr,
+         int64_t ws_off = 0) {
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
   ojx::GemmParams p;
   p.W = static_cast<const uint16_t*>(w);
@@ -140,8 +203,30 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.tiles_n = (int)cdiv(N, t->bn);
   p.tiles_m = (int)cdiv(M, t->bm);
   p.splits = c.splitk;
+  p.sk_ws = nullptr;
+  p.sk_cnt = nullptr;
+  p.dp_tiles = 0;
+  p.sk_grid = 0;
+  {
+    static int dbg = -1;
+    if (dbg < 0) { const char* e = getenv("OJX_DEBUG"); dbg = e ? atoi(e) : 0; }
+    p.dbg = dbg;
+  }
+  int grid = 0;
+  if (t->family == 5) {
+    const SkPlan sp = sk_plan(t, M, N, K, c.splitk);
+    p.splits = 1;
+    p.dp_tiles = sp.dp;
+    p.sk_grid = sp.gs;
+    grid = sp.grid;
+    if (sp.partial) {
+      if (ws == nullptr) return fail(OJX_ERR_WORKSPACE, "stream-K plan needs a workspace");
+      p.sk_cnt = static_cast<uint32_t*>(ws);
+      p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off);
+    }
+  }
   if ((int64_t)p.tiles_n * p.tiles_m * p.splits >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "grid too large");
-  return hip_check(ojx::launch_gemm(c.tile, epi, p, st), "gemm launch");
+  return hip_check(ojx::launch_gemm(c.tile, epi, p, st, grid), "gemm launch");
 }
 
 int check_operands(const void* x, const void* w, int64_t ldx, int64_t ldw, int64_t K) {
@@ -243,7 +328,7 @@ int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, oj
 int64_t ojx_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg) {
   ojx_cfg c{};
   if (resolve(M, N, K, kind, cfg, &c) != OJX_OK) return -1;
-  return workspace_for(c, M, N);
+  return workspace_for(c, M, N, K);
 }
 
 int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
@@ -256,16 +341,17 @@ int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, i
     return fail(OJX_ERR_ARG, "y must be 8-byte aligned with row stride >= N and a multiple of 4");
   ojx_cfg c{};
   OJX_TRY(resolve(M, N, K, OJX_KIND_PLAIN, cfg, &c));
-  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N)));
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   Part parts[2];
-  const int np = split_parts(c, M, N, parts);
+  const int np = split_parts(c, M, N, K, parts);
   for (int i = 0; i < np; ++i) {
     const Part& q = parts[i];
     const void* wq = static_cast<const uint16_t*>(w) + q.n0 * ldw;
     uint16_t* yq = static_cast<uint16_t*>(y) + q.n0;
-    if (q.c.splitk == 1) {
-      OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st));
+    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
+      OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st,
+                   workspace, q.ws));
       continue;
     }
     float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
@@ -283,8 +369,14 @@ int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, i
   OJX_TRY(check_operands(x, w, ldx, ldw, K));
   if (parts == nullptr || !aligned(parts, 16)) return fail(OJX_ERR_ARG, "parts must be 16-byte aligned");
   ojx_cfg c{};
-  if (tile < 0) OJX_TRY(ojx_plan(M, N, K, OJX_KIND_RESIDUAL, &c));
-  else c.tile = tile;
+  if (tile < 0) {
+    OJX_TRY(ojx_plan(M, N, K, OJX_KIND_RESIDUAL, &c));
+    if (is_sk(c.tile)) c = heuristic_plan(M, N, K, OJX_KIND_RESIDUAL);  // that family writes no K planes
+  } else {
+    c.tile = tile;
+  }
+  if (is_sk(c.tile))
+    return fail(OJX_ERR_CONFIG, "tile %d (persistent stream-K family) has no split-K planes", c.tile);
   c.splitk = S;
   if (!cfg_fits(M, N, K, c))
     return fail(OJX_ERR_CONFIG, "split-K S=%d (tile %d) invalid for K=%lld", S, c.tile, (long long)K);
@@ -301,16 +393,17 @@ int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t
   if (out == nullptr || !aligned(out, 8)) return fail(OJX_ERR_ARG, "out must be 8-byte aligned");
   ojx_cfg c{};
   OJX_TRY(resolve(M, N, K, OJX_KIND_SILU_MUL, cfg, &c));
-  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N)));
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   Part parts[2];
-  const int np = split_parts(c, M, N, parts);
+  const int np = split_parts(c, M, N, K, parts);
   for (int i = 0; i < np; ++i) {
     const Part& q = parts[i];
     const void* wq = static_cast<const uint16_t*>(w_gu_packed) + q.n0 * K;
     uint16_t* oq = static_cast<uint16_t*>(out) + q.n0 / 2;  // packed blocks of 8 rows give 4 output columns
-    if (q.c.splitk == 1) {
-      OJX_TRY(gemm(q.c, ojx::EPI_SILU, x, K, wq, K, oq, I, nullptr, 0, M, q.n, K, st));
+    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
+      OJX_TRY(gemm(q.c, ojx::EPI_SILU, x, K, wq, K, oq, I, nullptr, 0, M, q.n, K, st,
+                   workspace, q.ws));
       continue;
     }
     float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
@@ -344,15 +437,16 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* h = static_cast<uint16_t*>(h_out);
   uint16_t* hn = static_cast<uint16_t*>(hn_out);
-  if (c.splitk == 1) {
-    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st));
+  if (c.splitk == 1 || is_sk(c.tile)) {
+    OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
+    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, kCntBytes));
     if (hn == nullptr) return OJX_OK;
     return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,
                                              (int)N, st), "rmsnorm launch");
   }
   if (hn == nullptr && N / 8 > 1024) return fail(OJX_ERR_SHAPE, "split-K residual needs N/8 <= 1024");
-  OJX_TRY(check_ws(workspace, workspace_bytes, (int64_t)c.splitk * M * N * 4));
-  float* parts = static_cast<float*>(workspace);
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
+  float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCntBytes);
   OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st));
   return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(residual), nullptr, parts, c.splitk, M * N,
                                            w1, rowmask, eps, h, hn, (int)M, (int)N, st), "rmsnorm launch");

@@ -18,116 +18,11 @@
 //   * XCD-aware block order: MI355X dispatches workgroup b to XCD (b mod 8). Blocks are renumbered so that each
 //     XCD runs a contiguous range of logical tiles, and the M tiles that share one W tile are adjacent in that
 //     range, so a W tile is fetched from HBM into that XCD's L2 once.
-#include "ojx_internal.h"
+#include "gemm_common.h"
 
 #include <type_traits>
 
 namespace ojx {
-
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-// Buffer loads: the descriptor's byte range makes out-of-range lanes read zeros without a branch, so predicated
-// tile loads stay in flight (a branch around each load would make the compiler drain the load queue at the join).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t bytes) {
-  const int32_t n = bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, n, 0x00020000);
-}
-__device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-}
-constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor's range: the load returns zeros
-
-// The same descriptor as four dwords, for loads issued from inline assembly. The compiler's wait-count pass does
-// not track those loads; the kernel that uses them waits for them itself with an explicit s_waitcnt vmcnt(N),
-// where N counts the loads it issued after them. (Untracked loads only ever make the compiler's own waits on its
-// tracked loads stricter, never looser.)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4 make_rsrc4(const void* base, int64_t bytes) {
-  const int32_t n = bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
-  r[2] = __builtin_amdgcn_readfirstlane((uint32_t)n);
-  r[3] = 0x00020000u;
-  return r;
-}
-__device__ __forceinline__ u32x4 bload_asm(const u32x4& r, uint32_t off) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(r) : "memory");
-  return v;
-}
-// Same load into accumulation registers (AGPRs): used for data that only goes on to LDS, so the compiler never has
-// a reason to copy or spill it before the explicit wait (it cannot tell that the load is still in flight).
-__device__ __forceinline__ u32x4 bload_asm_agpr(const u32x4& r, uint32_t off) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=a"(v) : "v"(off), "s"(r) : "memory");
-  return v;
-}
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-// 16-byte global -> LDS DMA: lane i of the wave writes lds + 16 i. (Kept out of the kernel templates: written
-// inline there, the address-space cast stops the host pass from emitting the kernels' launch stubs.)
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
-}
-
-// Workgroup barrier that orders LDS only. __syncthreads() is a full workgroup fence, which on gfx9 waits for every
-// outstanding global load (vmcnt(0)) and would drain the weight prefetch queue at each x-tile handoff.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
-
-// Epilogue of 4 consecutive outputs y[m][n .. n+3] (n a multiple of 4) held by one lane. For the fused SiLU.mul,
-// `u` is the partner lane's values: packed W_gu rows come in blocks of 8 (4 gate rows, then the 4 up rows of the
-// same columns), so a lane holding gate columns (`gate` true) finds its up columns in the partner lane.
-__device__ __forceinline__ void store4(const GemmParams& p, const int epi, const int z, const int m, const int n,
-                                       const bool gate, const f32x4 v, const f32x4 u) {
-  if (m >= p.M || n >= p.N) return;
-  if (epi == EPI_SILU) {
-    if (!gate) return;
-    uint32_t o[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(v[e]))) * rbf(u[e]));
-    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
-    *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-  } else if (epi == EPI_F32) {
-    float* dst = reinterpret_cast<float*>(p.out) + z * p.part_stride + (int64_t)m * p.ldo + n;
-    *reinterpret_cast<float4*>(dst) = make_float4(v[0], v[1], v[2], v[3]);
-  } else {
-    uint32_t o[4];
-    if (epi == EPI_RESID) {
-      const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
-      const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = f2bf(rv[e] + rbf(v[e]));
-    } else {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = f2bf(v[e]);
-    }
-    uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
-    *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-  }
-}
-
-__device__ __forceinline__ f32x4 shfl4(const f32x4 v, int mask) {
-  return f32x4{__shfl_xor(v[0], mask), __shfl_xor(v[1], mask), __shfl_xor(v[2], mask), __shfl_xor(v[3], mask)};
-}
-
-// Epilogue of one 16x16 accumulator fragment: lane holds v[e] = y[m][n + e]; lane group lg = lane / 16.
-__device__ __forceinline__ void store_tile(const GemmParams& p, const int epi, const int z, const int m, const int n,
-                                           const int lg, const f32x4 v) {
-  const f32x4 u = epi == EPI_SILU ? shfl4(v, 16) : v;  // all lanes take part in the exchange
-  store4(p, epi, z, m, n, (lg & 1) == 0, v, u);
-}
 
 template <int BN, int BM, int BK, int WN, int WM>
 __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams p, const int epi) {
@@ -897,6 +792,10 @@ struct TileEntry {
 #define OJX_W32D(FN, FM, WN, WM, DG)                                                                         \
   {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 128, 4},                      \
    gemm_w32d_kernel<FN, FM, WN, WM, DG>}
+// Persistent stream-K tiles: BN = WN*FN*16 W rows, BM = WM*FM*16 x rows, 64-k stages, two LDS buffers
+#define OJX_SK(FN, FM, WN, WM)                                                                               \
+  {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 2 * (WN * FN * 16 + WM * FM * 16) * 128, 5},    \
+   gemm_sk_kernel<FN, FM, WN, WM>}
 #define OJX_W32(FN, FM, WN, WM, DG)                                                                          \
   {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 72 * 2, 3},                   \
    gemm_w32_kernel<FN, FM, WN, WM, DG>}
@@ -979,6 +878,12 @@ static const TileEntry kTiles[] = {
     OJX_W32D(2, 4, 4, 1, 2),        // 70 256 x 128
     OJX_W32D(2, 5, 2, 2, 2),        // 71 128 x 320
     OJX_W32D(1, 9, 4, 1, 2),        // 72 128 x 288
+    OJX_SK(8, 4, 2, 4),             // 73 256 x 256 persistent, stream-K remainder
+    OJX_SK(4, 9, 4, 2),             // 74 256 x 288
+    OJX_SK(4, 4, 4, 2),             // 75 256 x 128
+    OJX_SK(4, 6, 4, 2),             // 76 256 x 192
+    OJX_SK(4, 3, 4, 2),             // 77 256 x 96
+    OJX_SK(2, 9, 4, 2),             // 78 128 x 288
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];
@@ -1011,11 +916,11 @@ hipError_t init_tiles() {
   return hipSuccess;
 }
 
-hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream) {
+hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream, int grid) {
   const TileEntry& e = kTiles[tile];
   hipError_t err = set_attr(tile);
   if (err != hipSuccess) return err;
-  const int grid = p.tiles_n * p.tiles_m * p.splits;
+  if (grid <= 0) grid = p.tiles_n * p.tiles_m * p.splits;
   hipLaunchKernelGGL(e.fn, dim3(grid), dim3(e.info.threads), e.info.lds_bytes, stream, p, epi);
   return hipGetLastError();
 }

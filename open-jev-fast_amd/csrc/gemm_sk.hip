@@ -1,0 +1,308 @@
+// Persistent bf16 projection GEMM for gfx950 with a stream-K remainder: y[M,N] = x[M,K] . W[N,K]^T, fp32
+// accumulation on v_mfma_f32_16x16x32_bf16, epilogues fused into the store (same modes as gemm.hip).
+//
+// Replaces the reference's cuBLASLt GEMM (src/lt.cpp:43-55, called through _mm, src/fastmodel.py:168-175) and its
+// split-K bmm (src/fastmodel.py:158-166) at the M where the projection stops being a pure weight stream.
+//
+// Why this shape of kernel:
+//   * Eight waves per workgroup, two per SIMD, each owning a (FN x 16) x (FM x 16) block of the output: while
+//     one wave waits on LDS or a barrier the other keeps the SIMD's MFMA pipe busy. The wave tiles are large
+//     (64x144, 128x64, ...) so that LDS operand traffic stays near 90 B/clk per CU, about half of what the
+//     LDS delivers on this part.
+//   * Both operand tiles go global -> LDS by DMA (buffer_load ... lds, 16 B per lane, one 8-row x 128 B block per
+//     wave instruction) in stages of 64 k, two LDS buffers: stage t+1 is in flight while stage t is multiplied, and
+//     no registers are spent on staging. LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row / 2) mod
+//     8, so the 16 rows that one ds_read_b128 touches land on 16 distinct bank groups.
+//   * W fragments are read one fragment ahead of the MFMAs that use them, so LDS latency hides behind MFMAs.
+//   * Persistent grid of one workgroup per CU. Tiles are first handed out in whole-tile waves of G (one tile per
+//     workgroup, XCD-aware order so that the M tiles of one W tile run on the same XCD at the same time and share
+//     its L2). The tiles left over (fewer than G) would leave most CUs idle for a whole tile time; instead their
+//     K iterations are split evenly over Gs workgroups (stream-K). A workgroup whose range covers only part of a
+//     tile writes its fp32 partial tile to a slot in the workspace and bumps the tile's arrival counter; the
+//     workgroup that arrives last sums the partials in ascending K order (deterministic whatever the arrival
+//     order), applies the epilogue and returns the counter to zero. No workgroup ever waits for another.
+#include "gemm_common.h"
+
+namespace ojx {
+
+namespace {
+
+constexpr int kSkMaxPieces = 64;  // pieces one stream-K tile may be split into (host-enforced)
+
+
+// Partial tiles and arrival counters are exchanged between workgroups that may sit on different XCDs, whose L2
+// caches are not coherent with each other. The exchange goes through memory with system-coherent (sc0 sc1)
+// vector accesses, which neither write back nor invalidate the L2 that the other workgroups' operands live in
+// (a device-scope fence would do both): relaxed agent-scope atomic loads and stores, which the compiler emits as
+// such accesses and still batches. A store is complete once vmcnt counts it down.
+// A fragment of a partial tile is stored as 4 planes of 64 lanes ([e][lane]), so that each 4-byte access
+// instruction covers 256 contiguous bytes.
+__device__ __forceinline__ void store_coherent(float* p, const f32x4 v) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) __hip_atomic_store(p + e * 64, v[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x4 load_coherent(const float* p) {
+  f32x4 v;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) v[e] = __hip_atomic_load(p + e * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return v;
+}
+__device__ __forceinline__ uint32_t atomic_add_coherent(uint32_t* p, uint32_t v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// First stream-K iteration of workgroup g when T iterations are shared by Gs workgroups (Gs <= T).
+__device__ __forceinline__ int64_t sk_start(int64_t g, int64_t T, int64_t Gs) { return g * T / Gs; }
+// The workgroup whose range holds iteration x: the largest g with sk_start(g) <= x.
+__device__ __forceinline__ int64_t sk_owner(int64_t x, int64_t T, int64_t Gs) { return ((x + 1) * Gs + T - 1) / T - 1; }
+
+// Instruction order of the main loop (see the stage loop in gemm_sk_kernel). Group g of a stage (2 FM groups of FN
+// MFMAs each: k32 step g / FM, x fragment g % FM) is preceded by its LDS reads: the x fragment of group g + 2 and
+// the step-1 W fragments assigned to it (fragment i is read in group i FM / FN).
+template <int FN, int FM>
+constexpr int sk_w1_reads(int g) {
+  int n = 0;
+  for (int i = 0; i < FN; ++i) n += (i * FM) / FN == g ? 1 : 0;
+  return n;
+}
+template <int G, int NGA, int FN, int FM>
+__device__ __forceinline__ void sk_sched() {
+  if constexpr (G < NGA) {
+    __builtin_amdgcn_sched_group_barrier(0x100, 1 + sk_w1_reads<FN, FM>(G), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
+    sk_sched<G + 1, NGA, FN, FM>();
+  }
+}
+
+}  // namespace
+
+template <int FN, int FM, int WN, int WM>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams p, const int epi) {
+  constexpr int NT = 64 * WN * WM;
+  constexpr int BN = WN * FN * 16, BM = WM * FM * 16;
+  constexpr int BK = 64, LS = BK + 8, ROWS = BN + BM;
+  constexpr int NW = WN * WM;
+  constexpr int RB = 128;                  // LDS bytes per row (64 k of bf16)
+  constexpr int STAGE = ROWS * RB;         // LDS bytes per stage
+  constexpr int NG = ROWS / 8;             // 8-row blocks per stage: one DMA instruction each
+  constexpr int GPW = (NG + NW - 1) / NW;  // DMA instructions per wave and stage (the last may be idle)
+  constexpr int GW = BN / 8 / NW;          // of which W blocks
+  static_assert((BN / 8) % NW == 0 && BM % 16 == 0, "W blocks must fill whole DMA rounds");
+  constexpr int FRAG = 256;                // floats per 16x16 fragment in a partial slot
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][ROWS][128 B], swizzled chunks
+  __shared__ int s_last;
+  __shared__ int s_slot[kSkMaxPieces];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wn = wave % WN, wm = wave / WN;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // kernel arguments used in the loops, as plain scalars
+  const int K = p.K, M = p.M, N = p.N;
+  const int tiles_m = p.tiles_m;
+  const int64_t ldw = p.ldw, ldx = p.ldx;
+  const uint16_t* const Wp = p.W;
+  const uint16_t* const Xp = p.X;
+
+  // XCD-aware logical id: the hardware sends workgroup b to XCD b mod 8; consecutive logical ids share an XCD.
+  const int G = gridDim.x, b = blockIdx.x;
+  const int q = G >> 3, r = G & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int ipt = (K + BK - 1) / BK;  // K iterations per tile
+  const int tiles = p.tiles_n * tiles_m;
+  const int dp = p.dp_tiles;
+
+  // DMA pattern: block gi = wave + i NW holds rows 8 gi .. 8 gi + 7; lane l fills row 8 gi + l / 8, physical
+  // chunk l % 8, which holds logical chunk (l % 8) ^ ((row / 2) % 8). (row / 2) % 8 = 4 (gi % 2) + l / 16, and
+  // gi % 2 = wave % 2 for every i.
+  const int kchunk = (lane & 7) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7);
+  const int kcol = kchunk * 8;  // k offset of this lane's chunk within a stage
+  uint32_t doff[GPW];           // byte offset of the lane's chunk at k = 0, within the tile's W or x rows
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    const int row = (wave + i * NW) * 8 + (lane >> 3);
+    doff[i] = i < GW ? (uint32_t)(row * ldw + kcol) * 2u : (uint32_t)((row - BN) * ldx + kcol) * 2u;
+  }
+  // fragment reads: row r0 + lr (r0 a multiple of 16), logical chunk 4 s + lg of k32 step s
+  const uint32_t ro0 = (uint32_t)(lr * RB + ((lg ^ (lr >> 1)) * 16));
+  const uint32_t ro1 = (uint32_t)(lr * RB + (((4 + lg) ^ (lr >> 1)) * 16));
+  const uint32_t wbase = (uint32_t)(wn * FN * 16 * RB), xbase = (uint32_t)((BN + wm * FM * 16) * RB);
+
+  // stream-K range of this workgroup
+  const int64_t T = (int64_t)(tiles - dp) * ipt;
+  const int64_t Gs = p.sk_grid;
+  const bool in_sk = T > 0 && L < Gs;
+  const int64_t my0 = in_sk ? sk_start(L, T, Gs) : 0, my1 = in_sk ? sk_start(L + 1, T, Gs) : 0;
+
+  f32x4 acc[FN][FM];
+  int tau_dp = L;
+  int64_t it = my0;
+  while (true) {
+    // ------------------------------------------------------------------ next segment: (tau, i0, i1)
+    int tau, i0, i1, ts = -1;
+    if (tau_dp < dp) {
+      tau = tau_dp;
+      i0 = 0;
+      i1 = ipt;
+      tau_dp += G;
+    } else if (it < my1) {
+      ts = (int)(it / ipt);
+      i0 = (int)(it - (int64_t)ts * ipt);
+      i1 = (int)min((int64_t)ipt, i0 + (my1 - it));
+      it += i1 - i0;
+      tau = dp + ts;
+    } else {
+      break;
+    }
+    tau = __builtin_amdgcn_readfirstlane(tau);
+    i0 = __builtin_amdgcn_readfirstlane(i0);
+    i1 = __builtin_amdgcn_readfirstlane(i1);
+    const int n0 = (tau / tiles_m) * BN, m0 = (tau % tiles_m) * BM;
+    const int kb = i0 * BK, ke = min(K, i1 * BK);
+    const int nk = i1 - i0;
+    // descriptors cover this tile's rows only: rows past N (or M) read zeros
+    const __amdgpu_buffer_rsrc_t rsW = make_rsrc(Wp + (int64_t)n0 * ldw, (int64_t)min(BN, N - n0) * ldw * 2);
+    const __amdgpu_buffer_rsrc_t rsX = make_rsrc(Xp + (int64_t)m0 * ldx, (int64_t)min(BM, M - m0) * ldx * 2);
+
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // ------------------------------------------------------------------ main loop
+#define OJX_SK_DMA(buf, k0)                                                                                \
+  do {                                                                                                     \
+    const bool ok_ = (k0) + kcol < ke;                                                                     \
+    const uint32_t kof_ = (uint32_t)(k0) * 2u;                                                             \
+    _Pragma("unroll") for (int i = 0; i < GPW; ++i) {                                                      \
+      if (GPW * NW == NG || wave + i * NW < NG)                                                            \
+        dma16(i < GW ? rsW : rsX, smem + (buf) * STAGE + (wave + i * NW) * 1024, ok_ ? doff[i] + kof_ : kOOB); \
+    }                                                                                                      \
+  } while (0)
+#define OJX_SK_W(sb, st, i) (*reinterpret_cast<const bf16x8*>((sb) + wbase + ((st) ? ro1 : ro0) + (i) * 16 * RB))
+#define OJX_SK_X(sb, g) (*reinterpret_cast<const bf16x8*>((sb) + xbase + (((g) / FM) ? ro1 : ro0) + ((g) % FM) * 16 * RB))
+
+    // Software pipeline across stages. A stage is 2 FM groups (k32 step s = g / FM, x fragment j = g % FM) of FN
+    // MFMAs; LDS reads run two groups ahead. The step-0 W fragments and the first two x fragments of stage t+1 are
+    // read right after the barrier that publishes stage t+1, while the last two groups of stage t (operands
+    // already in registers) keep the MFMA pipe busy.
+    constexpr int NGR = 2 * FM;
+    static_assert(FM >= 2, "the last two groups of a stage must be k32 step 1");
+    OJX_SK_DMA(0, kb);
+    wait_vmcnt<0>();
+    lds_barrier();
+    if (nk > 1) OJX_SK_DMA(1, kb + BK);
+    bf16x8 a0c[FN], xn0, xn1;
+#pragma unroll
+    for (int i = 0; i < FN; ++i) a0c[i] = OJX_SK_W(smem, 0, i);
+    xn0 = OJX_SK_X(smem, 0);
+    xn1 = OJX_SK_X(smem, 1);
+    for (int t = 0; t < nk; ++t) {
+      const uint8_t* sb = smem + (t & 1) * STAGE;
+      bf16x8 a1c[FN], xr[3];
+      xr[0] = xn0;
+      xr[1] = xn1;
+#pragma unroll
+      for (int g = 0; g < NGR - 2; ++g) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          if ((i * FM) / FN == g) a1c[i] = OJX_SK_W(sb, 1, i);
+        xr[(g + 2) % 3] = OJX_SK_X(sb, g + 2);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          acc[i][g % FM] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g < FM ? a0c[i] : a1c[i], xr[g % 3],
+                                                                   acc[i][g % FM], 0, 0, 0);
+      }
+      sk_sched<0, NGR - 2, FN, FM>();
+      if (t + 1 < nk) {
+        wait_vmcnt<0>();  // this wave's DMA of stage t+1 has landed
+        lds_barrier();    // every wave's has, and every wave's reads of stage t are complete
+        if (t + 2 < nk && !(p.dbg & 1)) OJX_SK_DMA(t & 1, kb + (t + 2) * BK);
+        const uint8_t* sn = smem + ((t + 1) & 1) * STAGE;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) a0c[i] = OJX_SK_W(sn, 0, i);
+        xn0 = OJX_SK_X(sn, 0);
+        xn1 = OJX_SK_X(sn, 1);
+      }
+#pragma unroll
+      for (int g = NGR - 2; g < NGR; ++g)
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+          acc[i][g % FM] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1c[i], xr[g % 3], acc[i][g % FM], 0, 0, 0);
+    }
+    lds_barrier();  // the next segment's first DMA reuses buffer 0
+#undef OJX_SK_W
+#undef OJX_SK_X
+#undef OJX_SK_DMA
+
+    // ------------------------------------------------------------------ partial tile: combine the pieces
+    if (i0 != 0 || i1 != ipt) {
+      // Pieces of stream-K tile ts belong to workgroups g0..g1 in K order; a workgroup keeps a tile's piece in
+      // slot 2g if the tile is where its range starts, else (its range ends inside the tile) in slot 2g+1.
+      const int64_t x0 = (int64_t)ts * ipt;
+      const int64_t g0 = sk_owner(x0, T, Gs), g1 = sk_owner(x0 + ipt - 1, T, Gs);
+      const int64_t frag0 = (int64_t)wave * FN * FM * FRAG + lane;
+      {
+        float* slot = p.sk_ws + (2 * L + (my0 >= x0 ? 0 : 1)) * (int64_t)(BN * BM) + frag0;
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+          for (int j = 0; j < FM; ++j) store_coherent(slot + (i * FM + j) * FRAG, acc[i][j]);
+      }
+      wait_vmcnt<0>();  // the partial has reached memory before it is counted
+      __syncthreads();
+      if (tid == 0) s_last = atomic_add_coherent(&p.sk_cnt[ts], 1u) == (uint32_t)(g1 - g0);
+      __syncthreads();
+      if (!s_last) continue;
+      const int np = (int)(g1 - g0 + 1);  // at most kSkMaxPieces (the host sizes Gs so)
+      if (tid < np) {
+        const int64_t g = g0 + tid;
+        s_slot[tid] = (int)(2 * g + (sk_start(g, T, Gs) >= x0 ? 0 : 1));
+      }
+      __syncthreads();
+      // fp32 addition commutes exactly; the association follows ascending K, ((p0 + p1) + p2) + ..., whichever
+      // workgroup arrived last, so the result does not depend on arrival order.
+      const int me = (int)(L - g0);
+#pragma unroll
+      for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+          f32x4 v = acc[i][j];
+          for (int k = 0; k < np; ++k) {
+            f32x4 u = acc[i][j];
+            if (k != me) u = load_coherent(p.sk_ws + (int64_t)s_slot[k] * (BN * BM) + frag0 + (i * FM + j) * FRAG);
+            v = k == 0 ? u : v + u;
+          }
+          acc[i][j] = v;
+        }
+      if (tid == 0) store_coherent_u32(&p.sk_cnt[ts], 0u);
+    }
+
+    // ------------------------------------------------------------------ epilogue
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+      for (int j = 0; j < FM; ++j) {
+        const int n = n0 + (wn * FN + i) * 16 + lg * 4;
+        const int m = m0 + (wm * FM + j) * 16 + lr;
+        store_tile(p, epi, 0, m, n, lg, acc[i][j]);
+      }
+  }
+}
+
+}  // namespace ojx
+
+namespace ojx {
+// Tile shapes of this family (registered in gemm.hip's tile table): BN x BM = (WN*FN*16) x (WM*FM*16).
+template __global__ void gemm_sk_kernel<8, 4, 2, 4>(const GemmParams, const int);  // 256 x 256
+template __global__ void gemm_sk_kernel<4, 9, 4, 2>(const GemmParams, const int);  // 256 x 288
+template __global__ void gemm_sk_kernel<4, 4, 4, 2>(const GemmParams, const int);  // 256 x 128
+template __global__ void gemm_sk_kernel<4, 6, 4, 2>(const GemmParams, const int);  // 256 x 192
+template __global__ void gemm_sk_kernel<4, 3, 4, 2>(const GemmParams, const int);  // 256 x 96
+template __global__ void gemm_sk_kernel<2, 9, 4, 2>(const GemmParams, const int);  // 128 x 288
+}  // namespace ojx

@@ -43,6 +43,12 @@ struct GemmParams {
   int M, N, K;
   int kchunk;                       // K elements per split (multiple of 8; the last split may be shorter)
   int tiles_n, tiles_m, splits;
+  // persistent stream-K kernels (family 5) only
+  float* sk_ws;                     // partial-tile slots, 2 per workgroup, BN*BM fp32 each
+  uint32_t* sk_cnt;                 // arrival counter per stream-K tile: zero on entry, left zero on exit
+  int dp_tiles;                     // tiles done whole first (a multiple of the grid)
+  int sk_grid;                      // workgroups that share the remaining tiles' K iterations
+  int dbg;                          // experiment switches (0 in production)
 };
 
 struct TileInfo {
@@ -50,14 +56,16 @@ struct TileInfo {
   int threads;
   int lds_bytes;
   int family;  // 0: both operands through LDS; 1: W streamed straight into registers, x through LDS; 2: LDS DMA;
-               // 3: 32x32 MFMA, W streamed, x staged through registers; 4: 32x32 MFMA, W streamed, x by DMA
+               // 3: 32x32 MFMA, W streamed, x staged through registers; 4: 32x32 MFMA, W streamed, x by DMA;
+               // 5: persistent, 2 waves per SIMD, whole-tile waves then stream-K over the remainder
 };
 
 // Tile registry (gemm.hip)
 int num_tiles();
 hipError_t init_tiles();  // sets the dynamic-LDS limit of every tile kernel
 const TileInfo* tile_info(int tile);
-hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream);
+// grid: workgroups to launch; 0 = one per (tile, split) (the persistent family passes its own)
+hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream, int grid = 0);
 
 // Row / elementwise kernels (epilogue.hip)
 hipError_t launch_reduce_bf16(const float* parts, int S, int64_t part_stride, uint16_t* y, int64_t ldy,

@@ -50,13 +50,28 @@ def _cfgp(cfg):
     return ctypes.byref(cfg)
 
 
+_WS = {}
+
+
 def _workspace(M, N, K, kind, cfg, device):
+    """Workspace of one call: split-K planes, or the stream-K arrival counters and partial slots.
+
+    The counters must be zero before a call and every call leaves them zero, so one zero-filled buffer per (device,
+    stream) is kept and grown as needed; calls on one stream are ordered, so they can share it. Under graph capture
+    the buffer comes from the graph's pool and its zero fill is recorded with the graph."""
     n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
     if n < 0:
         check(1)
     if n == 0:
         return None, 0
-    return torch.empty(n, dtype=torch.uint8, device=device), n
+    if torch.cuda.is_current_stream_capturing():
+        return torch.zeros(n, dtype=torch.uint8, device=device), n
+    key = (torch.device(device).index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < n:
+        ws = torch.zeros(max(n, 1 << 20), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws, ws.numel()
 
 
 # ------------------------------------------------------------------------------------------------ epilogues
