@@ -80,7 +80,7 @@ struct SkPlan {
 SkPlan sk_plan(const ojx::TileInfo* t, int64_t M, int64_t N, int64_t K, int32_t S) {
   SkPlan sp{};
   const int64_t tiles = cdiv(N, t->bn) * cdiv(M, t->bm);
-  const int64_t ipt = cdiv(K, 64);
+  const int64_t ipt = cdiv(K, t->bk);  // the family's K per stream-K iteration
   const int64_t G = device_cus();
   const int64_t dp = (tiles / G) * G, R = tiles - dp;
   int64_t gs = 0;

@@ -12,8 +12,10 @@
 //   * Both operand tiles go global -> LDS by DMA (buffer_load ... lds, 16 B per lane, one 8-row x 128 B block per
 //     wave instruction) in stages of 64 k, two LDS buffers: stage t+1 is in flight while stage t is multiplied, and
 //     no registers are spent on staging. LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row / 2) mod
-//     8, so the 16 rows that one ds_read_b128 touches land on 16 distinct bank groups.
-//   * W fragments are read one fragment ahead of the MFMAs that use them, so LDS latency hides behind MFMAs.
+//     8, so the 16 rows that one ds_read_b128 touches land on 16 distinct bank groups. (Stages of 32 k with four
+//     buffers were measured slower: twice the barriers, and no gain from the deeper DMA queue.)
+//   * The operand with fewer fragments per wave stays in registers for a stage; the other one's fragments are read
+//     two MFMA groups ahead, so LDS latency hides behind MFMAs.
 //   * Persistent grid of one workgroup per CU. Tiles are first handed out in whole-tile waves of G (one tile per
 //     workgroup, XCD-aware order so that the M tiles of one W tile run on the same XCD at the same time and share
 //     its L2). The tiles left over (fewer than G) would leave most CUs idle for a whole tile time; instead their
@@ -54,26 +56,32 @@ __device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Workgroup barrier for the DMA pipeline: LDS reads of this wave complete, then s_barrier. The DMAs of later
+// stages stay in flight (a release fence on LDS would wait for every outstanding LDS DMA, vmcnt(0)); the caller
+// has already waited, with an explicit vmcnt, for the DMAs of the stage this barrier publishes.
+__device__ __forceinline__ void dma_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // First stream-K iteration of workgroup g when T iterations are shared by Gs workgroups (Gs <= T).
 __device__ __forceinline__ int64_t sk_start(int64_t g, int64_t T, int64_t Gs) { return g * T / Gs; }
 // The workgroup whose range holds iteration x: the largest g with sk_start(g) <= x.
 __device__ __forceinline__ int64_t sk_owner(int64_t x, int64_t T, int64_t Gs) { return ((x + 1) * Gs + T - 1) / T - 1; }
 
-// Instruction order of the main loop (see the stage loop in gemm_sk_kernel). Group g of a stage (2 FM groups of FN
-// MFMAs each: k32 step g / FM, x fragment g % FM) is preceded by its LDS reads: the x fragment of group g + 2 and
-// the step-1 W fragments assigned to it (fragment i is read in group i FM / FN).
-template <int FN, int FM>
-constexpr int sk_w1_reads(int g) {
+// Instruction order of the main loop before its barrier (see the stage loop in gemm_sk_kernel). Group g of a stage
+// (2 NR groups of NS MFMAs each: k32 step g / NR, streaming fragment g % NR) is preceded by its LDS reads: the
+// streaming fragment of group g + PD and the step-1 stationary fragments assigned to it (fragment q is read in
+// group q NR / NS).
+template <int NS, int NR>
+constexpr int sk_s1_reads(int g) {
   int n = 0;
-  for (int i = 0; i < FN; ++i) n += (i * FM) / FN == g ? 1 : 0;
+  for (int q = 0; q < NS; ++q) n += (q * NR) / NS == g ? 1 : 0;
   return n;
 }
-template <int G, int NGA, int FN, int FM>
-__device__ __forceinline__ void sk_sched() {
+template <int G, int NGA, int NS, int NR>
+__device__ __forceinline__ void sk_sched() {  // NGA = groups before the barrier
   if constexpr (G < NGA) {
-    __builtin_amdgcn_sched_group_barrier(0x100, 1 + sk_w1_reads<FN, FM>(G), 0);
-    __builtin_amdgcn_sched_group_barrier(0x008, FN, 0);
-    sk_sched<G + 1, NGA, FN, FM>();
+    __builtin_amdgcn_sched_group_barrier(0x100, 1 + sk_s1_reads<NS, NR>(G), 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
+    sk_sched<G + 1, NGA, NS, NR>();
   }
 }
 
@@ -81,17 +89,16 @@ __device__ __forceinline__ void sk_sched() {
 
 template <int FN, int FM, int WN, int WM>
 __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams p, const int epi) {
-  constexpr int NT = 64 * WN * WM;
   constexpr int BN = WN * FN * 16, BM = WM * FM * 16;
-  constexpr int BK = 64, LS = BK + 8, ROWS = BN + BM;
+  constexpr int BK = 64, ROWS = BN + BM;
   constexpr int NW = WN * WM;
-  constexpr int RB = 128;                  // LDS bytes per row (64 k of bf16)
-  constexpr int STAGE = ROWS * RB;         // LDS bytes per stage
-  constexpr int NG = ROWS / 8;             // 8-row blocks per stage: one DMA instruction each
-  constexpr int GPW = (NG + NW - 1) / NW;  // DMA instructions per wave and stage (the last may be idle)
-  constexpr int GW = BN / 8 / NW;          // of which W blocks
+  constexpr int RB = 128;                       // LDS bytes per row (64 k of bf16)
+  constexpr int STAGE = ROWS * RB;              // LDS bytes per stage
+  constexpr int NBLK = ROWS / 8;                // 8-row blocks per stage: one DMA instruction each
+  constexpr int GPW = (NBLK + NW - 1) / NW;     // DMA instructions per wave and stage
+  constexpr int GW = BN / 8 / NW;               // of which W blocks
   static_assert((BN / 8) % NW == 0 && BM % 16 == 0, "W blocks must fill whole DMA rounds");
-  constexpr int FRAG = 256;                // floats per 16x16 fragment in a partial slot
+  constexpr int FRAG = 256;                     // floats per 16x16 fragment in a partial slot
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][ROWS][128 B], swizzled chunks
   __shared__ int s_last;
@@ -113,21 +120,20 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
   const int G = gridDim.x, b = blockIdx.x;
   const int q = G >> 3, r = G & 7, xcd = b & 7;
   const int L = xcd * q + min(xcd, r) + (b >> 3);
-  const int ipt = (K + BK - 1) / BK;  // K iterations per tile
+  const int ipt = (K + BK - 1) / BK;  // K iterations (stages) per tile
   const int tiles = p.tiles_n * tiles_m;
   const int dp = p.dp_tiles;
 
   // DMA pattern: block gi = wave + i NW holds rows 8 gi .. 8 gi + 7; lane l fills row 8 gi + l / 8, physical
   // chunk l % 8, which holds logical chunk (l % 8) ^ ((row / 2) % 8). (row / 2) % 8 = 4 (gi % 2) + l / 16, and
-  // gi % 2 = wave % 2 for every i.
-  const int kchunk = (lane & 7) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7);
-  const int kcol = kchunk * 8;  // k offset of this lane's chunk within a stage
-  uint32_t doff[GPW];           // byte offset of the lane's chunk at k = 0, within the tile's W or x rows
-#pragma unroll
-  for (int i = 0; i < GPW; ++i) {
-    const int row = (wave + i * NW) * 8 + (lane >> 3);
-    doff[i] = i < GW ? (uint32_t)(row * ldw + kcol) * 2u : (uint32_t)((row - BN) * ldx + kcol) * 2u;
-  }
+  // gi % 2 = wave % 2 for every i (NW is even). Waves with fewer than GPW blocks repeat the last block (identical
+  // bytes to the same place), so every wave issues GPW DMAs per stage.
+  const int kcol = ((lane & 7) ^ ((((wave & 1) << 2) | (lane >> 4)) & 7)) * 8;  // k of this lane's chunk
+  const int kcoll = ((lane & 7) ^ (((((NBLK - 1) & 1) << 2) | (lane >> 4)) & 7)) * 8;  // same, in the last block
+  const uint32_t dW0 = (uint32_t)(((wave * 8 + (lane >> 3)) * ldw + kcol) * 2);
+  const uint32_t dX0 = (uint32_t)(((wave * 8 + (lane >> 3)) * ldx + kcol) * 2);
+  const uint32_t dXl = (uint32_t)((((NBLK - 1) * 8 - BN + (lane >> 3)) * ldx + kcoll) * 2);
+  uint32_t stepW = (uint32_t)(NW * 8 * ldw * 2), stepX = (uint32_t)(NW * 8 * ldx * 2);
   // fragment reads: row r0 + lr (r0 a multiple of 16), logical chunk 4 s + lg of k32 step s
   const uint32_t ro0 = (uint32_t)(lr * RB + ((lg ^ (lr >> 1)) * 16));
   const uint32_t ro1 = (uint32_t)(lr * RB + (((4 + lg) ^ (lr >> 1)) * 16));
@@ -177,67 +183,83 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
     // ------------------------------------------------------------------ main loop
 #define OJX_SK_DMA(buf, k0)                                                                                \
   do {                                                                                                     \
-    const bool ok_ = (k0) + kcol < ke;                                                                     \
-    const uint32_t kof_ = (uint32_t)(k0) * 2u;                                                             \
+    const uint32_t kof_ = (p.dbg & 2) ? 0u : (uint32_t)(k0) * 2u;                                          \
+    /* keep the per-block offsets as one multiply-add each instead of GPW registers held across the loop */ \
+    asm volatile("" : "+s"(stepW), "+s"(stepX));                                                           \
     _Pragma("unroll") for (int i = 0; i < GPW; ++i) {                                                      \
-      if (GPW * NW == NG || wave + i * NW < NG)                                                            \
-        dma16(i < GW ? rsW : rsX, smem + (buf) * STAGE + (wave + i * NW) * 1024, ok_ ? doff[i] + kof_ : kOOB); \
+      const bool real_ = GPW * NW == NBLK || wave + i * NW < NBLK;                                         \
+      const uint32_t o_ = i < GW ? dW0 + i * stepW : real_ ? dX0 + (i - GW) * stepX : dXl;                 \
+      const bool ok_ = (k0) + (real_ ? kcol : kcoll) < ke;                                                 \
+      const int blk_ = real_ ? wave + i * NW : NBLK - 1;                                                   \
+      dma16(i < GW ? rsW : rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);              \
     }                                                                                                      \
   } while (0)
-#define OJX_SK_W(sb, st, i) (*reinterpret_cast<const bf16x8*>((sb) + wbase + ((st) ? ro1 : ro0) + (i) * 16 * RB))
-#define OJX_SK_X(sb, g) (*reinterpret_cast<const bf16x8*>((sb) + xbase + (((g) / FM) ? ro1 : ro0) + ((g) % FM) * 16 * RB))
+    // Fragment reads. The stationary operand (the one with fewer fragments per wave: W if FN <= FM, else x) is
+    // held for a whole k32 step; the streaming operand's fragments are read PD groups ahead of their MFMAs.
+    constexpr bool XST = FN > FM;
+    constexpr int NS = XST ? FM : FN, NR = XST ? FN : FM;
+#define OJX_SK_FRAG(sb, base, st, f) (*reinterpret_cast<const bf16x8*>((sb) + (base) + ((st) ? ro1 : ro0) + (f) * 16 * RB))
+#define OJX_SK_S(sb, st, q) OJX_SK_FRAG(sb, XST ? xbase : wbase, st, q)
+#define OJX_SK_R(sb, g) OJX_SK_FRAG(sb, XST ? wbase : xbase, (g) / NR, (g) % NR)
+#define OJX_SK_MFMA(q, r, sv, rv)                                                                          \
+  do {                                                                                                     \
+    if constexpr (XST) acc[r][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rv, sv, acc[r][q], 0, 0, 0);    \
+    else acc[q][r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(sv, rv, acc[q][r], 0, 0, 0);                  \
+  } while (0)
 
-    // Software pipeline across stages. A stage is 2 FM groups (k32 step s = g / FM, x fragment j = g % FM) of FN
-    // MFMAs; LDS reads run two groups ahead. The step-0 W fragments and the first two x fragments of stage t+1 are
-    // read right after the barrier that publishes stage t+1, while the last two groups of stage t (operands
-    // already in registers) keep the MFMA pipe busy.
-    constexpr int NGR = 2 * FM;
-    static_assert(FM >= 2, "the last two groups of a stage must be k32 step 1");
+    // Software pipeline across stages. A stage (64 k) is 2 NR groups (k32 step g / NR, streaming fragment g % NR)
+    // of NS MFMAs. Stage t+1 is in flight by DMA while stage t is multiplied. The step-0 stationary fragments and
+    // the first PD streaming fragments of stage t+1 are read right after the barrier that publishes it, while the
+    // last PD groups of stage t (operands already in registers) keep the MFMA pipe busy; the buffer of stage t is
+    // refilled with stage t+2 right after that barrier, by which point every wave has read it.
+    constexpr int NGR = 2 * NR;
+    constexpr int PD = NR < 2 ? NR : 2;  // prefetch distance in groups = trailing groups after the barrier
+    constexpr int XR = PD + 1;           // streaming fragment ring
     OJX_SK_DMA(0, kb);
-    wait_vmcnt<0>();
-    lds_barrier();
     if (nk > 1) OJX_SK_DMA(1, kb + BK);
-    bf16x8 a0c[FN], xn0, xn1;
+    if (nk > 1) wait_vmcnt<GPW>();  // stage 0 has landed; stage 1 may be in flight
+    else wait_vmcnt<0>();
+    dma_barrier();
+    bf16x8 s0c[NS], rn[PD];
 #pragma unroll
-    for (int i = 0; i < FN; ++i) a0c[i] = OJX_SK_W(smem, 0, i);
-    xn0 = OJX_SK_X(smem, 0);
-    xn1 = OJX_SK_X(smem, 1);
+    for (int q = 0; q < NS; ++q) s0c[q] = OJX_SK_S(smem, 0, q);
+#pragma unroll
+    for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(smem, d);
     for (int t = 0; t < nk; ++t) {
       const uint8_t* sb = smem + (t & 1) * STAGE;
-      bf16x8 a1c[FN], xr[3];
-      xr[0] = xn0;
-      xr[1] = xn1;
+      bf16x8 s1c[NS], rr[XR];
 #pragma unroll
-      for (int g = 0; g < NGR - 2; ++g) {
+      for (int d = 0; d < PD; ++d) rr[d] = rn[d];
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
-          if ((i * FM) / FN == g) a1c[i] = OJX_SK_W(sb, 1, i);
-        xr[(g + 2) % 3] = OJX_SK_X(sb, g + 2);
+      for (int g = 0; g < NGR - PD; ++g) {
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
-          acc[i][g % FM] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(g < FM ? a0c[i] : a1c[i], xr[g % 3],
-                                                                   acc[i][g % FM], 0, 0, 0);
+        for (int qq = 0; qq < NS; ++qq)
+          if ((qq * NR) / NS == g) s1c[qq] = OJX_SK_S(sb, 1, qq);
+        rr[(g + PD) % XR] = OJX_SK_R(sb, g + PD);
+#pragma unroll
+        for (int qq = 0; qq < NS; ++qq) OJX_SK_MFMA(qq, g % NR, g < NR ? s0c[qq] : s1c[qq], rr[g % XR]);
       }
-      sk_sched<0, NGR - 2, FN, FM>();
+      sk_sched<0, NGR - PD, NS, NR>();
       if (t + 1 < nk) {
         wait_vmcnt<0>();  // this wave's DMA of stage t+1 has landed
-        lds_barrier();    // every wave's has, and every wave's reads of stage t are complete
+        dma_barrier();    // every wave's has, and every wave's reads of stage t are done
         if (t + 2 < nk && !(p.dbg & 1)) OJX_SK_DMA(t & 1, kb + (t + 2) * BK);
-        const uint8_t* sn = smem + ((t + 1) & 1) * STAGE;
+        const uint8_t* sx = smem + ((t + 1) & 1) * STAGE;
 #pragma unroll
-        for (int i = 0; i < FN; ++i) a0c[i] = OJX_SK_W(sn, 0, i);
-        xn0 = OJX_SK_X(sn, 0);
-        xn1 = OJX_SK_X(sn, 1);
+        for (int qq = 0; qq < NS; ++qq) s0c[qq] = OJX_SK_S(sx, 0, qq);
+#pragma unroll
+        for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(sx, d);
       }
 #pragma unroll
-      for (int g = NGR - 2; g < NGR; ++g)
+      for (int g = NGR - PD; g < NGR; ++g)
 #pragma unroll
-        for (int i = 0; i < FN; ++i)
-          acc[i][g % FM] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1c[i], xr[g % 3], acc[i][g % FM], 0, 0, 0);
+        for (int qq = 0; qq < NS; ++qq) OJX_SK_MFMA(qq, g % NR, s1c[qq], rr[g % XR]);
     }
-    lds_barrier();  // the next segment's first DMA reuses buffer 0
-#undef OJX_SK_W
-#undef OJX_SK_X
+    dma_barrier();  // the next segment's first DMAs reuse buffer 0
+#undef OJX_SK_FRAG
+#undef OJX_SK_S
+#undef OJX_SK_R
+#undef OJX_SK_MFMA
 #undef OJX_SK_DMA
 
     // ------------------------------------------------------------------ partial tile: combine the pieces
