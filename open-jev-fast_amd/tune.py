@@ -50,8 +50,10 @@ def main():
     ap.add_argument("--max-waves", type=float, default=16.0, help="skip candidates with more workgroups than this "
                     "many per CU")
     ap.add_argument("--no-tails", action="store_true", help="simple (tile, split-K) candidates only")
+    ap.add_argument("--sk-splits", default="1,2,4,8", help="stream-K spreads tried for the persistent family")
     args = ap.parse_args()
     Ms = [int(m) for m in args.m.split(",")] if args.m else list(M_DEFAULT)
+    sk_splits = {int(v) for v in args.sk_splits.split(",")}
     names = args.shapes.split(",") if args.shapes else list(TUNE_SHAPES)
     rows = []
     dev = "cuda"
@@ -87,9 +89,13 @@ def main():
                 if only is not None and c.tile not in only:
                     continue
                 info = _lib.tile_info(c.tile)
-                wgs = -(-N // info["bn"]) * -(-M // info["bm"]) * c.splitk
-                if wgs > args.max_waves * 256:
-                    continue
+                if info["family"] == 5:  # persistent: one workgroup per CU; splitk is the stream-K spread
+                    if c.splitk not in sk_splits:
+                        continue
+                else:
+                    wgs = -(-N // info["bn"]) * -(-M // info["bm"]) * c.splitk
+                    if wgs > args.max_waves * 256:
+                        continue
                 timed((c.tile, c.splitk, 0, 1, 0))
             if kind != "residual" and not args.no_tails:
                 # tail configurations: the best simple tiles over whole rounds of 256 workgroups, the leftover
@@ -99,10 +105,11 @@ def main():
                 for t, key in simple:
                     if len(seen) == 4:
                         break
-                    if key[0] not in seen:
+                    if key[0] not in seen and _lib.tile_info(key[0])["family"] != 5:
                         seen.append(key[0])
                         mains += [(key[0], 1), (key[0], 2)]
-                tails = [c for c in _lib.candidates(M, N, K, kid) if c.splitk <= 4 and (only is None or c.tile in only)]
+                tails = [c for c in _lib.candidates(M, N, K, kid) if c.splitk <= 4 and (only is None or c.tile in only)
+                         and _lib.tile_info(c.tile)["family"] != 5]
                 for tile, S in mains:
                     info = _lib.tile_info(tile)
                     per_tile = -(-M // info["bm"]) * S

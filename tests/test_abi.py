@@ -47,11 +47,19 @@ def test_plan_valid_for_every_contract_shape(pkg, kind):
         c = pkg._lib.plan(M, N, K, kind)
         assert 0 <= c.tile < L.ojx_num_tiles() and 1 <= c.splitk <= 16
         ws = pkg._lib.workspace_bytes(M, N, K, kind)
-        if pkg._lib.tile_info(c.tile)["family"] == 5:  # persistent stream-K: counters + partial slots, or nothing
-            assert ws == 0 or ws > 4096
-        else:  # 4 KiB of stream-K counters, then the split-K planes (256-byte multiple)
-            planes = -(-c.splitk * M * N * 4 // 256) * 256
-            assert ws == (4096 + planes if c.splitk > 1 else 0)
+        # 4 KiB of stream-K counters, then each launch's data: split-K planes (256-byte multiple) or, for the
+        # persistent family, partial-tile slots (or nothing)
+        parts = [(c.tile, c.splitk, N - c.tail_rows)] + ([(c.tail_tile, c.tail_splitk, c.tail_rows)] if c.tail_rows else [])
+        data, sk = 0, False
+        for tile, S, n in parts:
+            if pkg._lib.tile_info(tile)["family"] == 5:
+                sk = True
+            elif S > 1:
+                data += -(-S * M * n * 4 // 256) * 256
+        if sk:
+            assert ws == 0 or ws >= 4096 + data
+        else:
+            assert ws == (4096 + data if data else 0)
 
 
 def test_candidates(pkg):

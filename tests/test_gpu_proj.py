@@ -288,3 +288,75 @@ def test_graph_capture_replays(pkg, ext, O, dev):
         junk = ext.mm(hn, w_in)  # eager work between replays
         torch.cuda.synchronize()
         del junk
+
+
+# ----------------------------------------------------------------------------------------------- persistent family
+def _sk_tiles(pkg):
+    return [t for t in _tiles(pkg) if pkg._lib.tile_info(t)["family"] == 5]
+
+
+@pytest.mark.parametrize("M,N,K", [(539, 16384, 512), (288, 4096, 2048), (64, 2048, 17408), (300, 264, 136)])
+def test_stream_k_family(pkg, ext, O, dev, M, N, K):
+    """Persistent tiles: whole-tile waves, then the remainder's K iterations spread over the grid (S = pieces per
+    tile). Every spread matches the oracle, repeats bit-exactly (the partials are summed in K order whatever the
+    arrival order), and leaves the workspace counters at zero for the next call."""
+    x, w = O.seeded_inputs(M, N, K, seed=M + N + K + 1)
+    ref = O.linear_bf16(x, w)
+    xd, wd = x.to(dev), w.to(dev)
+    for t in _sk_tiles(pkg):
+        base = None
+        for S in (1, 2, 8, 16):
+            _say(f"case stream-K M={M} N={N} K={K} tile={t} S={S}")
+            y = ext.mm(xd, wd, cfg=(t, S))
+            _assert_tol(O, y, ref, f"tile {t} S {S}")
+            assert torch.equal(y, ext.mm(xd, wd, cfg=(t, S))), f"tile {t} S {S} not deterministic"
+            if S == 1:
+                base = y
+        for ws in ext._WS.values():
+            assert int(ws[:4096].count_nonzero()) == 0, "stream-K counters not returned to zero"
+        assert base is not None
+
+
+def test_stream_k_epilogues_and_graph(pkg, ext, O, dev):
+    """Fused SiLU.mul and residual epilogues through the persistent family with a stream-K remainder, eager and in
+    a replayed graph (the arrival counters must return to zero on every replay)."""
+    M, I, K, N = 288, 1032, 640, 1024
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wd = (torch.randn(N, K, generator=g) * 0.01).bfloat16()
+    res = torch.randn(M, N, generator=g).bfloat16()
+    w1 = (1.0 + 0.1 * torch.randn(N, generator=g)).float()
+    ref_silu = O.gate_up_silu(x, wg, wu)
+    rh, rhn = O.residual_proj(res, x, wd, w1, None, 1e-6, S=1)
+    xd, packed = x.to(dev), ext.pack_gate_up(wg.to(dev), wu.to(dev))
+    for t in _sk_tiles(pkg):
+        for S in (1, 4):
+            _say(f"case stream-K epilogues tile={t} S={S}")
+            out = ext.mm_silu_mul(xd, packed, cfg=(t, S))
+            _assert_tol(O, out, ref_silu, f"silu tile {t} S {S}")
+            h, hn = ext.mm_residual_rmsnorm(res.to(dev), xd, wd.to(dev), w1.to(dev), None, 1e-6, cfg=(t, S))
+            _assert_tol(O, h, rh, f"h tile {t} S {S}")
+            _assert_tol(O, hn, rhn, f"hn tile {t} S {S}")
+    t = _sk_tiles(pkg)[-1]
+    cfg = (t, 4)
+    eager = ext.mm_silu_mul(xd, packed, cfg=cfg).clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ext.mm_silu_mul(xd, packed, cfg=cfg)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("case stream-K graph capture")
+    with torch.cuda.graph(graph):
+        out = ext.mm_silu_mul(xd, packed, cfg=cfg)
+    for r in range(4):
+        _say(f"case stream-K graph replay {r}")
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {r} differs"
+        junk = ext.mm_silu_mul(xd, packed, cfg=cfg)  # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.equal(junk, eager)
