@@ -137,16 +137,20 @@ def main_default(args, pkg, ext, perf):
     r = perf.roofline(M, N, K, "silu", ms * 1e-3)
     flops, nbytes = perf.work(M, N, K, "silu")
 
-    # Per-launch duration of the dominant kernel (the GEMM), HIP events on the stream it is launched on. With a
-    # split-K plan the call is GEMM (fp32 partials) + reduce/SiLU.mul; the GEMM pass is then timed alone through
-    # ojx_gemm_splitk_f32 with the same tile and split, which launches the same kernel with the same grid.
+    # Per-launch duration of the dominant kernel: the GEMM launch over the plan's main rows (all W rows but the
+    # tail, when the plan has one), timed with HIP events on the stream it is launched on. It is launched alone
+    # through the C-ABI with the same tile, split and grid as inside the call: with split-K that is the fp32
+    # partial pass (ojx_gemm_splitk_f32), otherwise the GEMM with the fused SiLU.mul epilogue on those rows.
     cur = torch.cuda.current_stream()
-    if plan.splitk > 1:
-        dom = [lambda w=w: ext.mm_splitk_f32(x, w, plan.splitk, tile=plan.tile) for w in ws]
+    n1 = N - plan.tail_rows
+    fam = pkg._lib.tile_info(plan.tile)["family"]
+    if plan.splitk > 1 and fam != 5:
+        dom = [lambda w=w: ext.mm_splitk_f32(x, w[:n1], plan.splitk, tile=plan.tile) for w in ws]
         dom_name = "gemm (split-K partial pass)"
     else:
-        dom = fns
+        dom = [lambda w=w: ext.mm_silu_mul(x, w[:n1], cfg=(plan.tile, plan.splitk)) for w in ws]
         dom_name = "gemm (fused SiLU.mul epilogue)"
+    dom_name += f", W rows 0..{n1} of {N}" if plan.tail_rows else ""
     for i in range(4):
         dom[i % 2]()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -158,16 +162,17 @@ def main_default(args, pkg, ext, perf):
     ev1.record(cur)
     torch.cuda.synchronize()
     k_s = ev0.elapsed_time(ev1) * 1e-3 / n_k
+    kflops, kbytes = perf.work(M, n1, K, "silu")
     bound = r["bound"]
     if bound == "hbm":
-        achieved, peak, unit = nbytes / k_s / 1e9, perf.HBM_PEAK / 1e9, "GB/s"
+        achieved, peak, unit = kbytes / k_s / 1e9, perf.HBM_PEAK / 1e9, "GB/s"
     else:
-        achieved, peak, unit = flops / k_s / 1e12, perf.MFMA_BF16_PEAK / 1e12, "TFLOP/s"
-    tkey = f"gate_up_silu_M{M}_tile{plan.tile}_s{plan.splitk}"
+        achieved, peak, unit = kflops / k_s / 1e12, perf.MFMA_BF16_PEAK / 1e12, "TFLOP/s"
+    tkey = f"gate_up_silu_M{M}_tile{plan.tile}_s{plan.splitk}_rows{n1}"
     roof = {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(tkey),
-            "kernel": dom_name, "kernel_us": round(k_s * 1e6, 2), "algorithmic_bytes": nbytes,
-            "algorithmic_flops": flops}
+            "kernel": dom_name, "kernel_us": round(k_s * 1e6, 2), "algorithmic_bytes": kbytes,
+            "algorithmic_flops": kflops}
     del ws, fns, dom, graph
 
     shapes = {}
@@ -184,7 +189,9 @@ def main_default(args, pkg, ext, perf):
         "data": "synthetic: seeded x ~ N(0,1), W ~ N(0,0.02^2), bf16; 2 rotating weight copies",
         "config": {"workload": "gate_up_silu: BASELINE configs[1], fused gate-up + SiLU.mul, M=288 K=5120 "
                                "I=17408 (W_gu 34816x5120)", "M": M, "N": N, "K": K,
-                   "plan": {"tile": plan.tile, "splitk": plan.splitk, **pkg._lib.tile_info(plan.tile)}},
+                   "plan": {"tile": plan.tile, "splitk": plan.splitk, **pkg._lib.tile_info(plan.tile),
+                            **({"tail_rows": plan.tail_rows, "tail_tile": plan.tail_tile,
+                                "tail_splitk": plan.tail_splitk} if plan.tail_rows else {})}},
         "gbs": round(r["gbs"], 1), "roofline_frac": round(r["frac"], 4),
         "roofline": roof, "cpu_baseline": cpu, "shapes": shapes,
     }

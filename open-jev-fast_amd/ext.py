@@ -56,21 +56,23 @@ _WS = {}
 def _workspace(M, N, K, kind, cfg, device):
     """Workspace of one call: split-K planes, or the stream-K arrival counters and partial slots.
 
-    The counters must be zero before a call and every call leaves them zero, so one zero-filled buffer per (device,
-    stream) is kept and grown as needed; calls on one stream are ordered, so they can share it. Under graph capture
-    the buffer comes from the graph's pool and its zero fill is recorded with the graph."""
+    The counters must be zero before a call and every call leaves them zero, so one zero-filled buffer per device
+    is kept and grown as needed (grown outside graph capture). Calls that run concurrently on different streams of
+    one device would share it: such callers use the C-ABI with a workspace of their own. When a graph capture needs
+    more than the kept buffer holds, the capture gets a buffer of its own whose zero fill is recorded with it."""
     n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
     if n < 0:
         check(1)
     if n == 0:
         return None, 0
+    key = torch.device(device).index
+    ws = _WS.get(key)
+    if ws is not None and ws.numel() >= n:
+        return ws, ws.numel()
     if torch.cuda.is_current_stream_capturing():
         return torch.zeros(n, dtype=torch.uint8, device=device), n
-    key = (torch.device(device).index, torch.cuda.current_stream(device).cuda_stream)
-    ws = _WS.get(key)
-    if ws is None or ws.numel() < n:
-        ws = torch.zeros(max(n, 1 << 20), dtype=torch.uint8, device=device)
-        _WS[key] = ws
+    ws = torch.zeros(max(n, 1 << 20), dtype=torch.uint8, device=device)
+    _WS[key] = ws
     return ws, ws.numel()
 
 
