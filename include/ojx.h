@@ -9,7 +9,9 @@
  * Every entry point returns OJX_OK (0) or an error code; ojx_last_error() gives the message of the last failure
  * on the calling thread. Launches go on the given stream, never synchronize and never allocate, so they can be
  * captured into a HIP graph. Entry points that take a workspace need ojx_workspace_bytes() bytes of device memory
- * there (0 bytes when the plan has no split-K).
+ * there (0 bytes when the plan has no split-K and no stream-K partial tiles). The first 4096 bytes of a workspace
+ * are stream-K arrival counters: they must be zero before the first call that uses the workspace (allocate it
+ * zero-filled once and keep it), and every call leaves them zero again. The rest is scratch for one call.
  *
  * Global state (the plan table, kernel attributes) is read-only after the first call; concurrent calls on
  * different streams are safe as long as they do not share output or workspace buffers.
@@ -61,8 +63,12 @@ int ojx_init(void);
 
 /* Tile registry: info7 = {BN (W rows), BM (x rows), BK, waves along N, waves along M, threads, family}.
  * Family: 0 both operands via LDS, 1 W streamed to registers, 2 LDS DMA (all 16x16x32 MFMA); 3 W streamed to
- * registers on 32x32x16 MFMA, 4 the same with x copied to LDS by DMA. Tiles of one MFMA shape sum K in the same order, so without split-K they give
- * bit-identical results; across MFMA shapes results agree to fp32 rounding. */
+ * registers on 32x32x16 MFMA, 4 the same with x copied to LDS by DMA; 5 persistent (one workgroup per CU, two
+ * waves per SIMD, LDS DMA, 16x16x32 MFMA): whole-tile waves, then the remaining tiles' K iterations spread over
+ * the grid (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles).
+ * Tiles of one MFMA shape sum K in the same order, so without split-K (stream-K spread 1 for family 5) they give
+ * bit-identical results; across MFMA shapes results agree to fp32 rounding. Stream-K results are deterministic:
+ * the pieces of a tile are summed in K order whatever order they finish in. */
 int ojx_num_tiles(void);
 int ojx_tile_info(int32_t tile, int32_t* info7);
 
