@@ -11,7 +11,7 @@ CPU baseline (the oracle's torch CPU path on a bounded sample of the same worklo
 per-shape table at M = 7 / 288 / 539 for the five projection shapes.
 
 Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
-the 64-layer projection stack at M = 539 in one graph replay).
+the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV).
 """
 import argparse
 import json
@@ -273,6 +273,24 @@ def main_stack(args, pkg, ext, perf):
           flush=True)
 
 
+def main_head(args, pkg, ext, perf):
+    """The scoring head (src/server.py:37): scores = hn[lastidx].float() @ w + b over the stack's M = 539 rows, for
+    R gathered rows. HBM-bound: algorithmic bytes R*H*2 (gathered rows) + H*4 (w) + R*4 (scores)."""
+    rows, H = 539, 5120
+    dev = "cuda"
+    g = torch.Generator(device=dev).manual_seed(7)
+    hn = torch.randn(rows, H, generator=g, device=dev).bfloat16()
+    w = torch.randn(H, generator=g, device=dev) * 0.02
+    b = torch.zeros(1, device=dev)
+    for R in (1, 16, 128, 539):
+        idx = torch.randint(0, rows, (R,), generator=g, device=dev)
+        t = perf.gpu_time([lambda: ext.head_scores(hn, idx, w, b)], iters=20, reps=5)
+        nbytes = R * H * 2 + H * 4 + R * 4
+        print(json.dumps({"head": "scoring head GEMV (gather + 5120 -> 1)", "R": R, "H": H, "us": round(t * 1e6, 2),
+                          "gbs": round(nbytes / t / 1e9, 1), "roof_us": round(nbytes / perf.HBM_PEAK * 1e6, 3),
+                          "frac": round(nbytes / perf.HBM_PEAK / t, 4)}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -280,6 +298,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--stack", action="store_true")
+    ap.add_argument("--head", action="store_true")
     ap.add_argument("--m", default="")
     ap.add_argument("--shapes", default="")
     ap.add_argument("--no-cpu", action="store_true")
@@ -298,6 +317,8 @@ def main():
         main_sweep(args, pkg, ext, perf)
     elif args.stack:
         main_stack(args, pkg, ext, perf)
+    elif args.head:
+        main_head(args, pkg, ext, perf)
     else:
         main_default(args, pkg, ext, perf)
 

@@ -115,6 +115,14 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
                               int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
                               ojx_stream_t stream);
 
+/* Scoring head: scores[r] = sum_j float(hn[lastidx[r]][j]) * w[j] + bias[0] (bias may be NULL), fp32.
+ * hn bf16 [rows, H] contiguous, lastidx int64 [R], w fp32 [H], scores fp32 [R]. Replaces the last matmul of the
+ * forward, mdl.head(hn[lastidx].float()).squeeze(-1) (src/server.py:37,57,129; hn[lastidx] is
+ * src/fastmodel.py:314,482), with the row gather fused in. An index outside [0, rows) gives NaN for that score
+ * (the reference's indexing would raise; a kernel cannot). H % 8 == 0. */
+int ojx_head_scores(const void* hn, int64_t rows, int64_t H, const int64_t* lastidx, int64_t R, const float* w,
+                    const float* bias, float* scores, ojx_stream_t stream);
+
 /* Standalone epilogues, same arguments and semantics as the reference extension's functions. */
 /* add_rmsnorm (src/kernels.cu:41-73, 755-767): delta may be NULL (then h_out is not written: h == x). */
 int ojx_add_rmsnorm(const void* x, const void* delta, const float* w1, const int32_t* rowmask, float eps,

@@ -49,6 +49,7 @@ EXPORTS = {
     "ojx_silu_mul": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
     "ojx_silu_mul_lut": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _p]),
     "ojx_act_tables": (ctypes.c_int, [_p, _p, _p]),
+    "ojx_head_scores": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _p, _p, _p, _p]),
     "ojx_pack_gate_up": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _p]),
 }
 

@@ -504,6 +504,19 @@ int ojx_silu_mul_lut(const void* gu, const void* tab, void* out, int64_t M, int6
   return silu_common(gu, tab, out, M, I, stream);
 }
 
+int ojx_head_scores(const void* hn, int64_t rows, int64_t H, const int64_t* lastidx, int64_t R, const float* w,
+                    const float* bias, float* scores, ojx_stream_t stream) {
+  if (R < 0 || rows < 0 || H <= 0 || H % 8 != 0)
+    return fail(OJX_ERR_SHAPE, "head needs H %% 8 == 0 (H=%lld), R, rows >= 0", (long long)H);
+  if (R == 0) return OJX_OK;
+  if (hn == nullptr || lastidx == nullptr || w == nullptr || scores == nullptr)
+    return fail(OJX_ERR_ARG, "null hn, lastidx, w or scores");
+  if (!aligned(hn, 16) || !aligned(w, 16) || !aligned(lastidx, 8) || !aligned(scores, 4))
+    return fail(OJX_ERR_ARG, "hn and w must be 16-byte aligned, lastidx 8-byte aligned");
+  return hip_check(ojx::launch_head_gemv(static_cast<const uint16_t*>(hn), rows, lastidx, R, w, bias, scores, (int)H,
+                                         static_cast<hipStream_t>(stream)), "head launch");
+}
+
 int ojx_act_tables(void* silu_b, float* sig_f, ojx_stream_t stream) {
   if (silu_b == nullptr || sig_f == nullptr) return fail(OJX_ERR_ARG, "null table output");
   return hip_check(ojx::launch_act_tables(static_cast<uint16_t*>(silu_b), sig_f, static_cast<hipStream_t>(stream)),

@@ -172,6 +172,48 @@ __global__ void __launch_bounds__(256) pack_gate_up_k(const uint16_t* __restrict
 
 static inline unsigned nblocks(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
+// Scoring head (src/server.py:37,57,129: mdl.head(hn[lastidx].float()).squeeze(-1), a Linear(H, 1) on fp32):
+// scores[r] = sum_j float(hn[lastidx[r]][j]) * w[j] (+ bias). One wave per score: lane l takes the 8-column
+// chunks l, l + 64, ... (16-byte coalesced loads), sums them in that order, then a fixed xor-butterfly across the
+// wave; the result is the same on every run. An index outside [0, rows) gives NaN and reads nothing.
+__global__ void __launch_bounds__(256) head_gemv_k(const uint16_t* __restrict__ hn, int64_t rows,
+                                                   const int64_t* __restrict__ lastidx, int64_t R,
+                                                   const float* __restrict__ w, const float* __restrict__ bias,
+                                                   float* __restrict__ scores, int H) {
+  const int lane = threadIdx.x & 63;
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= R) return;  // whole wave
+  const int64_t row = lastidx[r];
+  if (row < 0 || row >= rows) {
+    if (lane == 0) scores[r] = __builtin_nanf("");
+    return;
+  }
+  const uint16_t* src = hn + row * H;
+  float acc = 0.f;
+  for (int c = lane; c < H / 8; c += 64) {
+    const uint4 v = *reinterpret_cast<const uint4*>(src + c * 8);
+    const float4 w0 = *reinterpret_cast<const float4*>(w + c * 8);
+    const float4 w1 = *reinterpret_cast<const float4*>(w + c * 8 + 4);
+    acc = fmaf(bf2f(v.x & 0xffffu), w0.x, acc);
+    acc = fmaf(bf2f(v.x >> 16), w0.y, acc);
+    acc = fmaf(bf2f(v.y & 0xffffu), w0.z, acc);
+    acc = fmaf(bf2f(v.y >> 16), w0.w, acc);
+    acc = fmaf(bf2f(v.z & 0xffffu), w1.x, acc);
+    acc = fmaf(bf2f(v.z >> 16), w1.y, acc);
+    acc = fmaf(bf2f(v.w & 0xffffu), w1.z, acc);
+    acc = fmaf(bf2f(v.w >> 16), w1.w, acc);
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (lane == 0) scores[r] = acc + (bias != nullptr ? bias[0] : 0.f);
+}
+
+hipError_t launch_head_gemv(const uint16_t* hn, int64_t rows, const int64_t* lastidx, int64_t R, const float* w,
+                            const float* bias, float* scores, int H, hipStream_t st) {
+  hipLaunchKernelGGL(head_gemv_k, dim3(nblocks(R, 4)), dim3(256), 0, st, hn, rows, lastidx, R, w, bias, scores, H);
+  return hipGetLastError();
+}
+
 hipError_t launch_reduce_bf16(const float* parts, int S, int64_t ps, uint16_t* y, int64_t ldy, int M, int N,
                               hipStream_t st) {
   const int64_t n = (int64_t)M * (N / 4);

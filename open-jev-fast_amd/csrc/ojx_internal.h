@@ -77,6 +77,8 @@ hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* delta_bf16, con
                               uint16_t* h_out, uint16_t* hn_out, int M, int H, hipStream_t st);
 hipError_t launch_silu_mul(const uint16_t* gu, const uint16_t* tab, uint16_t* out, int M, int I, hipStream_t st);
 hipError_t launch_act_tables(uint16_t* silu_b, float* sig_f, hipStream_t st);
+hipError_t launch_head_gemv(const uint16_t* hn, int64_t rows, const int64_t* lastidx, int64_t R, const float* w,
+                            const float* bias, float* scores, int H, hipStream_t st);
 hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* packed, int I, int K,
                                hipStream_t st);
 

@@ -9,6 +9,7 @@ functions, for the entry points on the projection path:
     silu_mul(gu) -> out                                       src/kernels.cu:76-89, 769-777
     silu_mul_lut(gu, tab) -> out                              src/kernels.cu:1304-1331
     act_tables(like) -> [silu_b, sig_f]                       src/kernels.cu:1288-1301
+    head_scores(hn, lastidx, w, bias) -> scores              src/server.py:37 (mdl.head(hn[lastidx].float()))
 
 plus the fused projections that replace GEMM + epilogue pairs (mm, mm_silu_mul, mm_residual_rmsnorm,
 mm_splitk_f32) and pack_gate_up, the weight layout of the fused gate-up.
@@ -203,6 +204,25 @@ def mm_residual_rmsnorm(h, y, w, w1, rowmask, eps, want_hn=True, cfg=None):
                                           float(eps), _ptr(h_new), _ptr(hn), M, N, K, _ptr(ws), nws, _cfgp(cfg),
                                           _stream()))
     return h_new, hn
+
+
+def head_scores(hn, lastidx, w, bias=None):
+    """scores [R] fp32 = hn[lastidx].float() @ w (+ bias): the scoring head, mdl.head(hn[lastidx].float())
+    .squeeze(-1) (src/server.py:37, 57, 129) for a Linear(H, 1) with fp32 weight w [H] (or [1, H]) and bias [1], with
+    the row gather fused in. lastidx is int64; an out-of-range index gives NaN for that score."""
+    _chk(hn, "hn", torch.bfloat16)
+    _chk(lastidx, "lastidx", torch.int64)
+    w = w.reshape(-1)
+    _chk(w, "w", torch.float32)
+    if bias is not None:
+        _chk(bias, "bias", torch.float32)
+    rows, H = hn.shape
+    if w.numel() != H:
+        raise RuntimeError(f"w has {w.numel()} elements, hn rows have {H}")
+    R = lastidx.numel()
+    scores = torch.empty(R, dtype=torch.float32, device=hn.device)
+    check(lib().ojx_head_scores(_ptr(hn), rows, H, _ptr(lastidx), R, _ptr(w), _ptr(bias), _ptr(scores), _stream()))
+    return scores
 
 
 def pack_gate_up(gate, up):

@@ -17,11 +17,16 @@ What it restates (reference file:line):
   pack_gate_up       the fused-GEMM weight layout (rows in blocks of 8: 4 gate rows, 4 up rows) — libojx's own
                      layout, restated here so tests can build it on the CPU
   linear_f64         fp64 brute-force dot products (numpy), the independent check the oracle is pinned against
+  head_scores        mdl.head(hn[lastidx].float()).squeeze(-1) (src/server.py:37, 57, 129; hn[lastidx] at
+                     src/fastmodel.py:314, 482) for a Linear(H, 1) with fp32 weight and bias: torch fp32 on the CPU.
+                     The head module belongs to the Open-Jev model package, which the reference does not vendor:
+                     Linear(H, 1) in fp32 is read off its call site (input cast .float(), output squeeze(-1)).
 
 Pinning (tests/test_oracle.py): linear_bf16 against linear_f64 and exact closed forms (identity, permutation,
 exactly representable rank-1 products); silu_mul against scipy's expit in fp64 and special values; add_rmsnorm
 against an fp64 RMSNorm and closed-form constant rows; the gate/up merge bit-exactness of tests/test_correct.py:44;
-splitk_parts summing to linear_f64. The reference holds no golden vectors for this path (no fixtures in its tree);
+splitk_parts summing to linear_f64; head_scores against fp64 dot products and one-hot weights (a gathered entry
+exactly), with the gather order checked by permuting lastidx. The reference holds no golden vectors for this path (no fixtures in its tree);
 tests/golden/ holds fp64 brute-force vectors made by tests/golden/make_golden.py.
 """
 import numpy as np
@@ -113,6 +118,19 @@ def pack_gate_up(gate, up):
     """[2I, K]: rows in blocks of 8 = gate rows 4b..4b+3 then up rows 4b..4b+3."""
     I, K = gate.shape
     return torch.stack([gate.view(I // 4, 4, K), up.view(I // 4, 4, K)], 1).reshape(2 * I, K)
+
+
+def head_scores(hn, lastidx, w, bias=None):
+    """scores [R] = hn[lastidx].float() @ w (+ bias), fp32 on the CPU (hn [rows, H] bf16, w [H] fp32)."""
+    s = torch.matmul(hn[lastidx].float(), w.reshape(-1).float())
+    return s + bias.reshape(()) if bias is not None else s
+
+
+def head_scores_f64(hn, lastidx, w, bias=None):
+    """fp64 brute force of head_scores (numpy)."""
+    a = hn[lastidx].float().numpy().astype(np.float64)
+    s = a @ w.reshape(-1).double().numpy()
+    return s + (float(bias.reshape(())) if bias is not None else 0.0)
 
 
 # ---------------------------------------------------------------------------------------------- inputs

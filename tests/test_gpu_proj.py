@@ -360,3 +360,28 @@ def test_stream_k_epilogues_and_graph(pkg, ext, O, dev):
         junk = ext.mm_silu_mul(xd, packed, cfg=cfg)  # eager work between replays
         torch.cuda.synchronize()
         assert torch.equal(junk, eager)
+
+
+# ----------------------------------------------------------------------------------------------- scoring head
+@pytest.mark.parametrize("R", [1, 7, 64, 539])
+def test_head_scores_vs_oracle(pkg, ext, O, dev, R):
+    """Fused gather + GEMV of the scoring head against the oracle (fp32 sums in another order: rel 1e-5), one-hot
+    weights exactly, deterministic, and NaN for an out-of-range index."""
+    g = torch.Generator().manual_seed(R)
+    rows, H = R + 50, 5120
+    hn = torch.randn(rows, H, generator=g).bfloat16()
+    w = torch.randn(H, generator=g) * 0.02
+    b = torch.tensor([-0.5])
+    idx = torch.randint(0, rows, (R,), generator=g)
+    _say(f"case head R={R}")
+    s = ext.head_scores(hn.to(dev), idx.to(dev), w.to(dev), b.to(dev)).cpu()
+    ref = torch.from_numpy(O.head_scores_f64(hn, idx, w, b)).float()
+    assert torch.allclose(s, ref, rtol=1e-5, atol=1e-5), (s - ref).abs().max()
+    assert torch.equal(s, ext.head_scores(hn.to(dev), idx.to(dev), w.to(dev), b.to(dev)).cpu())
+    e = torch.zeros(H)
+    e[123] = 1.0
+    assert torch.equal(ext.head_scores(hn.to(dev), idx.to(dev), e.to(dev)).cpu(), hn[idx, 123].float())
+    bad = idx.clone()
+    bad[0] = rows
+    sb = ext.head_scores(hn.to(dev), bad.to(dev), w.to(dev), b.to(dev)).cpu()
+    assert torch.isnan(sb[0]) and torch.equal(sb[1:], s[1:])

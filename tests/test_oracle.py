@@ -211,3 +211,23 @@ def test_tolerance_function():
     bad[0, 0] += 10 * r.abs().max()
     assert not O.tolerance_ok(bad, r)[0]
     assert not O.tolerance_ok(r + 0.01 * r.pow(2).mean().sqrt(), r)[0]   # mean error 1e-2 RMS
+
+
+# ----------------------------------------------------------------------------------------------- scoring head
+def test_head_scores_oracle_pinned(O):
+    """head_scores against fp64 dot products, one-hot weights (the gathered entry exactly) and a permuted gather."""
+    g = torch.Generator().manual_seed(3)
+    rows, H, R = 40, 5120, 9
+    hn = torch.randn(rows, H, generator=g).bfloat16()
+    w = torch.randn(H, generator=g) * 0.02
+    b = torch.tensor([0.25])
+    idx = torch.randint(0, rows, (R,), generator=g)
+    s = O.head_scores(hn, idx, w, b)
+    ref = torch.from_numpy(O.head_scores_f64(hn, idx, w, b))
+    assert torch.allclose(s.double(), ref, rtol=1e-5, atol=1e-5)
+    for j in (0, 17, H - 1):
+        e = torch.zeros(H)
+        e[j] = 1.0
+        assert torch.equal(O.head_scores(hn, idx, e), hn[idx, j].float())
+    perm = torch.randperm(R, generator=g)
+    assert torch.allclose(O.head_scores(hn, idx[perm], w, b), s[perm], rtol=1e-6, atol=1e-6)
