@@ -65,7 +65,8 @@ int ojx_init(void);
  * Family: 0 both operands via LDS, 1 W streamed to registers, 2 LDS DMA (all 16x16x32 MFMA); 3 W streamed to
  * registers on 32x32x16 MFMA, 4 the same with x copied to LDS by DMA; 5 persistent (one workgroup per CU, two
  * waves per SIMD, LDS DMA, 16x16x32 MFMA): whole-tile waves, then the remaining tiles' K iterations spread over
- * the grid (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles).
+ * the grid (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles);
+ * split tiles are summed by a second, small launch.
  * Tiles of one MFMA shape sum K in the same order, so without split-K (stream-K spread 1 for family 5) they give
  * bit-identical results; across MFMA shapes results agree to fp32 rounding. Stream-K results are deterministic:
  * the pieces of a tile are summed in K order whatever order they finish in. */

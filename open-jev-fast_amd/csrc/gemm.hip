@@ -781,6 +781,7 @@ typedef void (*GemmFn)(const GemmParams, const int);
 struct TileEntry {
   TileInfo info;
   GemmFn fn;
+  GemmFn fixup = nullptr;  // persistent family: second pass over the split stream-K tiles
 };
 
 #define OJX_TILE(BN, BM, BK, WN, WM)                                                                         \
@@ -795,7 +796,7 @@ struct TileEntry {
 // Persistent stream-K tiles: BN = WN*FN*16 W rows, BM = WM*FM*16 x rows, 64-k stages, two LDS buffers
 #define OJX_SK(FN, FM, WN, WM)                                                                               \
   {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 2 * (WN * FN * 16 + WM * FM * 16) * 128, 5},    \
-   gemm_sk_kernel<FN, FM, WN, WM>}
+   gemm_sk_kernel<FN, FM, WN, WM>, gemm_sk_fixup_kernel<FN, FM, WN, WM>}
 #define OJX_W32(FN, FM, WN, WM, DG)                                                                          \
   {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 72 * 2, 3},                   \
    gemm_w32_kernel<FN, FM, WN, WM, DG>}
@@ -922,6 +923,10 @@ hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t strea
   if (err != hipSuccess) return err;
   if (grid <= 0) grid = p.tiles_n * p.tiles_m * p.splits;
   hipLaunchKernelGGL(e.fn, dim3(grid), dim3(e.info.threads), e.info.lds_bytes, stream, p, epi);
+  err = hipGetLastError();
+  if (err != hipSuccess || e.fixup == nullptr || p.sk_ws == nullptr) return err;
+  const int rem = p.tiles_n * p.tiles_m - p.dp_tiles;  // the stream-K tiles
+  hipLaunchKernelGGL(e.fixup, dim3(rem), dim3(e.info.threads), 0, stream, p, epi);
   return hipGetLastError();
 }
 

@@ -117,4 +117,6 @@ namespace ojx {
 // Persistent stream-K family (gemm_sk.hip; instantiated there for the shapes of the tile table).
 template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_kernel(const GemmParams p, const int epi);
+template <int FN, int FM, int WN, int WM>
+__global__ void gemm_sk_fixup_kernel(const GemmParams p, const int epi);
 }  // namespace ojx

@@ -20,9 +20,10 @@
 //     workgroup, XCD-aware order so that the M tiles of one W tile run on the same XCD at the same time and share
 //     its L2). The tiles left over (fewer than G) would leave most CUs idle for a whole tile time; instead their
 //     K iterations are split evenly over Gs workgroups (stream-K). A workgroup whose range covers only part of a
-//     tile writes its fp32 partial tile to a slot in the workspace and bumps the tile's arrival counter; the
-//     workgroup that arrives last sums the partials in ascending K order (deterministic whatever the arrival
-//     order), applies the epilogue and returns the counter to zero. No workgroup ever waits for another.
+//     tile writes its fp32 partial tile to a slot in the workspace; a second, small launch sums each split
+//     tile's pieces in ascending K order (deterministic) and applies the epilogue. No workgroup ever waits for
+//     another, and the GEMM carries no cross-workgroup code: an in-kernel last-arrival reduction was measured
+//     (its registers cost the main loop spills, and its coherent stores bypassing L2 cost more than a launch).
 #include "gemm_common.h"
 
 namespace ojx {
@@ -31,30 +32,6 @@ namespace {
 
 constexpr int kSkMaxPieces = 64;  // pieces one stream-K tile may be split into (host-enforced)
 
-
-// Partial tiles and arrival counters are exchanged between workgroups that may sit on different XCDs, whose L2
-// caches are not coherent with each other. The exchange goes through memory with system-coherent (sc0 sc1)
-// vector accesses, which neither write back nor invalidate the L2 that the other workgroups' operands live in
-// (a device-scope fence would do both): relaxed agent-scope atomic loads and stores, which the compiler emits as
-// such accesses and still batches. A store is complete once vmcnt counts it down.
-// A fragment of a partial tile is stored as 4 planes of 64 lanes ([e][lane]), so that each 4-byte access
-// instruction covers 256 contiguous bytes.
-__device__ __forceinline__ void store_coherent(float* p, const f32x4 v) {
-#pragma unroll
-  for (int e = 0; e < 4; ++e) __hip_atomic_store(p + e * 64, v[e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ f32x4 load_coherent(const float* p) {
-  f32x4 v;
-#pragma unroll
-  for (int e = 0; e < 4; ++e) v[e] = __hip_atomic_load(p + e * 64, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return v;
-}
-__device__ __forceinline__ uint32_t atomic_add_coherent(uint32_t* p, uint32_t v) {
-  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent_u32(uint32_t* p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // Workgroup barrier for the DMA pipeline: LDS reads of this wave complete, then s_barrier. The DMAs of later
 // stages stay in flight (a release fence on LDS would wait for every outstanding LDS DMA, vmcnt(0)); the caller
@@ -101,8 +78,6 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
   constexpr int FRAG = 256;                     // floats per 16x16 fragment in a partial slot
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][ROWS][128 B], swizzled chunks
-  __shared__ int s_last;
-  __shared__ int s_slot[kSkMaxPieces];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -262,47 +237,19 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
 #undef OJX_SK_MFMA
 #undef OJX_SK_DMA
 
-    // ------------------------------------------------------------------ partial tile: combine the pieces
+    // ------------------------------------------------------------------ partial tile: to its slot
     if (i0 != 0 || i1 != ipt) {
       // Pieces of stream-K tile ts belong to workgroups g0..g1 in K order; a workgroup keeps a tile's piece in
       // slot 2g if the tile is where its range starts, else (its range ends inside the tile) in slot 2g+1.
+      // gemm_sk_fixup_kernel, launched right after this kernel, sums the pieces and applies the epilogue.
       const int64_t x0 = (int64_t)ts * ipt;
-      const int64_t g0 = sk_owner(x0, T, Gs), g1 = sk_owner(x0 + ipt - 1, T, Gs);
-      const int64_t frag0 = (int64_t)wave * FN * FM * FRAG + lane;
-      {
-        float* slot = p.sk_ws + (2 * L + (my0 >= x0 ? 0 : 1)) * (int64_t)(BN * BM) + frag0;
-#pragma unroll
-        for (int i = 0; i < FN; ++i)
-#pragma unroll
-          for (int j = 0; j < FM; ++j) store_coherent(slot + (i * FM + j) * FRAG, acc[i][j]);
-      }
-      wait_vmcnt<0>();  // the partial has reached memory before it is counted
-      __syncthreads();
-      if (tid == 0) s_last = atomic_add_coherent(&p.sk_cnt[ts], 1u) == (uint32_t)(g1 - g0);
-      __syncthreads();
-      if (!s_last) continue;
-      const int np = (int)(g1 - g0 + 1);  // at most kSkMaxPieces (the host sizes Gs so)
-      if (tid < np) {
-        const int64_t g = g0 + tid;
-        s_slot[tid] = (int)(2 * g + (sk_start(g, T, Gs) >= x0 ? 0 : 1));
-      }
-      __syncthreads();
-      // fp32 addition commutes exactly; the association follows ascending K, ((p0 + p1) + p2) + ..., whichever
-      // workgroup arrived last, so the result does not depend on arrival order.
-      const int me = (int)(L - g0);
+      float* slot = p.sk_ws + (2 * L + (my0 >= x0 ? 0 : 1)) * (int64_t)(BN * BM) +
+                    (int64_t)wave * FN * FM * FRAG + lane * 4;
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j) {
-          f32x4 v = acc[i][j];
-          for (int k = 0; k < np; ++k) {
-            f32x4 u = acc[i][j];
-            if (k != me) u = load_coherent(p.sk_ws + (int64_t)s_slot[k] * (BN * BM) + frag0 + (i * FM + j) * FRAG);
-            v = k == 0 ? u : v + u;
-          }
-          acc[i][j] = v;
-        }
-      if (tid == 0) store_coherent_u32(&p.sk_cnt[ts], 0u);
+        for (int j = 0; j < FM; ++j) *reinterpret_cast<f32x4*>(slot + (i * FM + j) * FRAG) = acc[i][j];
+      continue;
     }
 
     // ------------------------------------------------------------------ epilogue
@@ -317,14 +264,55 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
   }
 }
 
+// Second pass of a stream-K plan, one workgroup per remaining tile (same waves and fragment ownership as the GEMM):
+// a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and applies the epilogue; a tile done
+// whole by one workgroup was finished by the GEMM. The pieces are visible here because the GEMM launch has ended.
+template <int FN, int FM, int WN, int WM>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmParams p, const int epi) {
+  constexpr int BN = WN * FN * 16, BM = WM * FM * 16, BK = 64, FRAG = 256;
+  __shared__ int s_slot[kSkMaxPieces];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wn = wave % WN, wm = wave / WN;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int ipt = (p.K + BK - 1) / BK;
+  const int ts = blockIdx.x;
+  const int64_t T = (int64_t)(p.tiles_n * p.tiles_m - p.dp_tiles) * ipt;
+  const int64_t Gs = p.sk_grid;
+  const int64_t x0 = (int64_t)ts * ipt;
+  const int64_t g0 = sk_owner(x0, T, Gs), g1 = sk_owner(x0 + ipt - 1, T, Gs);
+  if (g0 == g1) return;
+  const int np = (int)(g1 - g0 + 1);  // at most kSkMaxPieces (the host sizes the grid so)
+  if (tid < np) {
+    const int64_t g = g0 + tid;
+    s_slot[tid] = (int)(2 * g + (sk_start(g, T, Gs) >= x0 ? 0 : 1));
+  }
+  __syncthreads();
+  const int tau = p.dp_tiles + ts;
+  const int n0 = (tau / p.tiles_m) * BN, m0 = (tau % p.tiles_m) * BM;
+  const float* base = p.sk_ws + (int64_t)wave * FN * FM * FRAG + lane * 4;
+  for (int i = 0; i < FN; ++i)
+    for (int j = 0; j < FM; ++j) {
+      const float* src = base + (i * FM + j) * FRAG;
+      f32x4 v = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[0] * (BN * BM));
+      for (int k = 1; k < np; ++k) v += *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[k] * (BN * BM));
+      store_tile(p, epi, 0, m0 + (wm * FM + j) * 16 + lr, n0 + (wn * FN + i) * 16 + lg * 4, lg, v);
+    }
+}
+
 }  // namespace ojx
 
 namespace ojx {
 // Tile shapes of this family (registered in gemm.hip's tile table): BN x BM = (WN*FN*16) x (WM*FM*16).
 template __global__ void gemm_sk_kernel<8, 4, 2, 4>(const GemmParams, const int);  // 256 x 256
+template __global__ void gemm_sk_fixup_kernel<8, 4, 2, 4>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<4, 9, 4, 2>(const GemmParams, const int);  // 256 x 288
+template __global__ void gemm_sk_fixup_kernel<4, 9, 4, 2>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<4, 4, 4, 2>(const GemmParams, const int);  // 256 x 128
+template __global__ void gemm_sk_fixup_kernel<4, 4, 4, 2>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<4, 6, 4, 2>(const GemmParams, const int);  // 256 x 192
+template __global__ void gemm_sk_fixup_kernel<4, 6, 4, 2>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<4, 3, 4, 2>(const GemmParams, const int);  // 256 x 96
+template __global__ void gemm_sk_fixup_kernel<4, 3, 4, 2>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<2, 9, 4, 2>(const GemmParams, const int);  // 128 x 288
+template __global__ void gemm_sk_fixup_kernel<2, 9, 4, 2>(const GemmParams, const int);
 }  // namespace ojx
