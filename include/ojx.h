@@ -10,8 +10,8 @@
  * on the calling thread. Launches go on the given stream, never synchronize and never allocate, so they can be
  * captured into a HIP graph. Entry points that take a workspace need ojx_workspace_bytes() bytes of device memory
  * there (0 bytes when the plan has no split-K and no stream-K partial tiles). The first 4096 bytes of a workspace
- * are stream-K arrival counters: they must be zero before the first call that uses the workspace (allocate it
- * zero-filled once and keep it), and every call leaves them zero again. The rest is scratch for one call.
+ * are reserved for arrival counters: keep them zero (allocate the workspace zero-filled once and reuse it); calls
+ * leave them zero. The rest is scratch for one call.
  *
  * Global state (the plan table, kernel attributes) is read-only after the first call; concurrent calls on
  * different streams are safe as long as they do not share output or workspace buffers.
