@@ -108,6 +108,11 @@ def test_argument_validation_without_gpu(pkg):
     assert L.ojx_pack_gate_up(p, p, p, 6, 64, None) == 2
     # M == 0 is a no-op
     assert L.ojx_gemm_bf16(p, p, p, 0, 64, 64, 64, 64, 64, None, 0, None, None) == 0
+    # scoring head: H % 8, null operands, misalignment; R == 0 is a no-op
+    assert L.ojx_head_scores(p, 4, 60, p, 3, p, None, p, None) == 2
+    assert L.ojx_head_scores(None, 4, 64, p, 3, p, None, p, None) == 1
+    assert L.ojx_head_scores(mis, 4, 64, p, 3, p, None, p, None) == 1
+    assert L.ojx_head_scores(p, 4, 64, p, 0, p, None, p, None) == 0
 
 
 def test_python_mirror_errors_without_gpu(pkg):

@@ -385,3 +385,33 @@ def test_head_scores_vs_oracle(pkg, ext, O, dev, R):
     bad[0] = rows
     sb = ext.head_scores(hn.to(dev), bad.to(dev), w.to(dev), b.to(dev)).cpu()
     assert torch.isnan(sb[0]) and torch.equal(sb[1:], s[1:])
+
+
+# ----------------------------------------------------------------------------------------------- full sizes
+@pytest.mark.parametrize("M", [7, 288, 539])
+def test_planned_full_size_projections(pkg, ext, O, dev, M):
+    """Every projection shape of the forward at the headline M, through the plan table's own
+    configuration (tails, split-K, stream-K included), against the oracle on the same seeded inputs."""
+    from importlib import import_module
+    perf = import_module("open_jev_fast_amd.perf")
+    g = torch.Generator().manual_seed(M)
+    for name, (N, K, kind) in perf.SHAPES.items():
+        _say(f"case full size {name} M={M} plan={pkg._lib.plan(M, N, K, {'plain': 0, 'silu': 1, 'residual': 2}[kind])}")
+        x = torch.randn(M, K, generator=g).bfloat16()
+        w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+        if kind == "plain":
+            out = ext.mm(x.to(dev), w.to(dev)).cpu()
+            ref = O.linear_bf16(x, w)
+            _assert_tol(O, out, ref, name)
+        elif kind == "silu":
+            I = N // 2
+            out = ext.mm_silu_mul(x.to(dev), ext.pack_gate_up(w[:I].to(dev), w[I:].to(dev))).cpu()
+            ref = O.gate_up_silu(x, w[:I], w[I:])
+            _assert_tol(O, out, ref, name)
+        else:
+            res = torch.randn(M, N, generator=g).bfloat16()
+            w1 = (1.0 + 0.1 * torch.randn(N, generator=g)).float()
+            h, hn = ext.mm_residual_rmsnorm(res.to(dev), x.to(dev), w.to(dev), w1.to(dev), None, 1e-6)
+            rh, rhn = O.residual_proj(res, x, w, w1, None, 1e-6, S=1)
+            _assert_tol(O, h.cpu(), rh, name + " h")
+            _assert_tol(O, hn.cpu(), rhn, name + " hn")
