@@ -169,9 +169,12 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
       dma16(i < GW ? rsW : rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);              \
     }                                                                                                      \
   } while (0)
-    // Fragment reads. The stationary operand (the one with fewer fragments per wave: W if FN <= FM, else x) is
-    // held for a whole k32 step; the streaming operand's fragments are read PD groups ahead of their MFMAs.
-    constexpr bool XST = FN > FM;
+    // Fragment reads. The stationary operand is held for a whole k32 step (both steps' fragments in registers);
+    // the streaming operand's fragments are read PD groups ahead of their MFMAs. The operand with more fragments
+    // per wave is made stationary when its two register sets fit beside the accumulators (more MFMAs per LDS
+    // read: each streaming read feeds NS MFMAs), else the other one.
+    constexpr bool BIG_X = FM > FN, FITS = FN * FM * 4 + 8 * (BIG_X ? FM : FN) <= 200;
+    constexpr bool XST = BIG_X == FITS;
     constexpr int NS = XST ? FM : FN, NR = XST ? FN : FM;
 #define OJX_SK_FRAG(sb, base, st, f) (*reinterpret_cast<const bf16x8*>((sb) + (base) + ((st) ? ro1 : ro0) + (f) * 16 * RB))
 #define OJX_SK_S(sb, st, q) OJX_SK_FRAG(sb, XST ? xbase : wbase, st, q)
