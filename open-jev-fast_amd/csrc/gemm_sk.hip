@@ -64,8 +64,10 @@ __device__ __forceinline__ void sk_sched() {  // NGA = groups before the barrier
 
 }  // namespace
 
-template <int FN, int FM, int WN, int WM>
-__global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams p, const int epi) {
+namespace {
+// The kernel body, specialised per epilogue mode (EPI) so that the epilogue is straight code for one mode.
+template <int FN, int FM, int WN, int WM, int EPI>
+__device__ __forceinline__ void sk_body(const GemmParams& p) {
   constexpr int BN = WN * FN * 16, BM = WM * FM * 16;
   constexpr int BK = 64, ROWS = BN + BM;
   constexpr int NW = WN * WM;
@@ -256,15 +258,70 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
     }
 
     // ------------------------------------------------------------------ epilogue
+    // Through LDS, P fragment columns at a time: the waves stage acc[i..i+P-1][*] (BM rows x WN strips of 16 P
+    // columns), then every thread applies the epilogue to IMAX items of 4 (SiLU: 8) consecutive columns, unrolled
+    // so that the items' LDS reads, math and stores overlap. The pass loop stays rolled: fully unrolled over the
+    // FN x FM fragments, the epilogue is tens of KB of straight-line code run once per tile, whose instruction
+    // fetches were measured to cost up to a quarter of the tile time.
+    {
+      constexpr int LDSB = 2 * STAGE;
+      constexpr int COLB = BM * (WN * 16 + 4) * 4;
+      constexpr int P = (FN % 4 == 0 && 4 * COLB <= LDSB) ? 4 : (FN % 2 == 0 && 2 * COLB <= LDSB) ? 2 : 1;
+      static_assert(COLB <= LDSB, "one staged fragment column must fit the LDS");
+      constexpr int SROW = WN * 16 * P + 4;  // floats per staged row (padded against bank conflicts)
+      constexpr bool SILU = EPI == EPI_SILU;
+      constexpr int CW = SILU ? 8 : 4;       // columns per item
+      constexpr int ITEMS = BM * WN * 16 * P / CW;
+      constexpr int IMAX = (ITEMS + 64 * NW - 1) / (64 * NW);
+      float* const stg = reinterpret_cast<float*>(smem);
+#pragma nounroll
+      for (int i = 0; i < FN; i += P) {
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+        for (int ii = 0; ii < FN; ii += P)
+          if (ii == i) {
 #pragma unroll
-      for (int j = 0; j < FM; ++j) {
-        const int n = n0 + (wn * FN + i) * 16 + lg * 4;
-        const int m = m0 + (wm * FM + j) * 16 + lr;
-        store_tile(p, epi, 0, m, n, lg, acc[i][j]);
+            for (int pp = 0; pp < P; ++pp)
+#pragma unroll
+              for (int j = 0; j < FM; ++j)
+                *reinterpret_cast<f32x4*>(stg + ((wm * FM + j) * 16 + lr) * SROW + (wn * P + pp) * 16 + lg * 4) =
+                    acc[ii + pp][j];
+          }
+        dma_barrier();
+        constexpr int IB = IMAX < 4 ? IMAX : 4;  // items in flight per thread (registers beside acc)
+#pragma unroll
+        for (int k0 = 0; k0 < IMAX; k0 += IB) {
+          f32x4 v[IB], u[IB];
+#pragma unroll
+          for (int k = 0; k < IB; ++k) {
+            const int e = min(tid + (k0 + k) * 64 * NW, ITEMS - 1);
+            const float* src = stg + (e / (WN * P * 16 / CW)) * SROW + (e % (WN * P * 16 / CW)) * CW;
+            v[k] = *reinterpret_cast<const f32x4*>(src);
+            if constexpr (SILU) u[k] = *reinterpret_cast<const f32x4*>(src + 4);
+            else u[k] = v[k];
+          }
+#pragma unroll
+          for (int k = 0; k < IB; ++k) {
+            const int e = tid + (k0 + k) * 64 * NW;
+            if (k0 + k >= IMAX || (ITEMS % (64 * NW) != 0 && e >= ITEMS)) continue;
+            const int m = e / (WN * P * 16 / CW), cc = (e % (WN * P * 16 / CW)) * CW;  // staged column
+            const int sp = cc >> 4;                                                   // strip = wn * P + pp
+            const int n = n0 + ((sp / P) * FN + i + sp % P) * 16 + (cc & 15);
+            store4(p, EPI, 0, m0 + m, n, true, v[k], u[k]);
+          }
+        }
+        dma_barrier();
       }
+    }
   }
+}
+
+}  // namespace
+
+template <int FN, int FM, int WN, int WM>
+__global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams p, const int epi) {
+  if (epi == EPI_SILU) sk_body<FN, FM, WN, WM, EPI_SILU>(p);
+  else if (epi == EPI_RESID) sk_body<FN, FM, WN, WM, EPI_RESID>(p);
+  else sk_body<FN, FM, WN, WM, EPI_BF16>(p);  // the host routes EPI_F32 (split-K planes) to other families
 }
 
 // Second pass of a stream-K plan, one workgroup per remaining tile (same waves and fragment ownership as the GEMM):
