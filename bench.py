@@ -140,7 +140,10 @@ def main_default(args, pkg, ext, perf):
     # Per-launch duration of the dominant kernel: the GEMM launch over the plan's main rows (all W rows but the
     # tail, when the plan has one), timed with HIP events on the stream it is launched on. It is launched alone
     # through the C-ABI with the same tile, split and grid as inside the call: with split-K that is the fp32
-    # partial pass (ojx_gemm_splitk_f32), otherwise the GEMM with the fused SiLU.mul epilogue on those rows.
+    # partial pass (ojx_gemm_splitk_f32), otherwise the GEMM with the fused SiLU.mul epilogue on those rows. For the
+    # persistent stream-K family the call is the GEMM plus the launch that sums the split tiles' pieces; the two
+    # are timed together (the GEMM cannot be launched without its fixup through the C-ABI), which understates the
+    # GEMM's own rate by the fixup's share.
     cur = torch.cuda.current_stream()
     n1 = N - plan.tail_rows
     fam = pkg._lib.tile_info(plan.tile)["family"]
@@ -149,7 +152,8 @@ def main_default(args, pkg, ext, perf):
         dom_name = "gemm (split-K partial pass)"
     else:
         dom = [lambda w=w: ext.mm_silu_mul(x, w[:n1], cfg=(plan.tile, plan.splitk)) for w in ws]
-        dom_name = "gemm (fused SiLU.mul epilogue)"
+        dom_name = ("persistent stream-K gemm (fused SiLU.mul epilogue) + split-tile fixup, one call of two "
+                    "launches" if fam == 5 else "gemm (fused SiLU.mul epilogue)")
     dom_name += f", W rows 0..{n1} of {N}" if plan.tail_rows else ""
     for i in range(4):
         dom[i % 2]()

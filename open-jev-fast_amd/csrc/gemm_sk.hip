@@ -53,12 +53,13 @@ constexpr int sk_s1_reads(int g) {
   for (int q = 0; q < NS; ++q) n += (q * NR) / NS == g ? 1 : 0;
   return n;
 }
-template <int G, int NGA, int NS, int NR>
-__device__ __forceinline__ void sk_sched() {  // NGA = groups before the barrier
-  if constexpr (G < NGA) {
+template <int G, int NGA, int NS, int NR, int DPG, int NDG>
+__device__ __forceinline__ void sk_sched() {  // NGA = groups before the barrier; DPG DMAs after the MFMAs of
+  if constexpr (G < NGA) {                    // each of the first NDG groups
     __builtin_amdgcn_sched_group_barrier(0x100, 1 + sk_s1_reads<NS, NR>(G), 0);
     __builtin_amdgcn_sched_group_barrier(0x008, NS, 0);
-    sk_sched<G + 1, NGA, NS, NR>();
+    if constexpr (G < NDG) __builtin_amdgcn_sched_group_barrier(0x020, DPG, 0);
+    sk_sched<G + 1, NGA, NS, NR, DPG, NDG>();
   }
 }
 
@@ -158,12 +159,12 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // ------------------------------------------------------------------ main loop
-#define OJX_SK_DMA(buf, k0)                                                                                \
+#define OJX_SK_DMA(buf, k0, lo, hi)                                                                        \
   do {                                                                                                     \
     const uint32_t kof_ = (p.dbg & 2) ? 0u : (uint32_t)(k0) * 2u;                                          \
     /* keep the per-block offsets as one multiply-add each instead of GPW registers held across the loop */ \
     asm volatile("" : "+s"(stepW), "+s"(stepX));                                                           \
-    _Pragma("unroll") for (int i = 0; i < GPW; ++i) {                                                      \
+    _Pragma("unroll") for (int i = (lo); i < (hi); ++i) {                                                  \
       const bool real_ = GPW * NW == NBLK || wave + i * NW < NBLK;                                         \
       const uint32_t o_ = i < GW ? dW0 + i * stepW : real_ ? dX0 + (i - GW) * stepX : dXl;                 \
       const bool ok_ = (k0) + (real_ ? kcol : kcoll) < ke;                                                 \
@@ -195,10 +196,20 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     constexpr int NGR = 2 * NR;
     constexpr int PD = NR < 2 ? NR : 2;  // prefetch distance in groups = trailing groups after the barrier
     constexpr int XR = PD + 1;           // streaming fragment ring
-    OJX_SK_DMA(0, kb);
-    if (nk > 1) OJX_SK_DMA(1, kb + BK);
-    if (nk > 1) wait_vmcnt<GPW>();  // stage 0 has landed; stage 1 may be in flight
-    else wait_vmcnt<0>();
+    // DMA issue: H0 of a stage's GPW DMA instructions right after the barrier that frees its buffer, the rest one
+    // at a time after the MFMAs of the next stage's first groups. Issued all at once, the DMAs of 8 waves fill the
+    // texture unit's command queue (measured full for a quarter of the kernel's cycles) and the waves stall at the
+    // issue with the MFMA pipe idle. A DMA issued inside a stage must still land before that stage's barrier, so
+    // spreading is limited to the groups that leave at least 16 MFMAs per SIMD (about 0.25 us) after the last one;
+    // tiles with less room issue everything after the barrier.
+    constexpr int NMG = NGR - PD;                  // groups before the barrier
+    constexpr int NA = NMG - (16 + NS - 1) / NS;   // groups that may carry a DMA
+    constexpr int H0 = NA <= 0 ? GPW : (GPW - NA > (GPW + 1) / 2 ? GPW - NA : (GPW + 1) / 2);
+    constexpr int DPG = H0 < GPW ? 1 : 0;          // DMAs per group
+    constexpr int NDG = GPW - H0;                  // groups that carry one
+    OJX_SK_DMA(0, kb, 0, GPW);
+    OJX_SK_DMA(1, kb + BK, 0, H0);  // the rest of stage 1 in stage 0's groups (zeros past ke)
+    wait_vmcnt<H0>();               // stage 0 has landed; stage 1 may be in flight
     dma_barrier();
     bf16x8 s0c[NS], rn[PD];
 #pragma unroll
@@ -207,23 +218,27 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(smem, d);
     for (int t = 0; t < nk; ++t) {
       const uint8_t* sb = smem + (t & 1) * STAGE;
+      const int kn = kb + (t + 1) * BK;  // stage t+1, into buffer (t+1)&1 (not read in this stage); past the
+                                         // segment's last stage the DMAs read zeros into the unused buffer
       bf16x8 s1c[NS], rr[XR];
 #pragma unroll
       for (int d = 0; d < PD; ++d) rr[d] = rn[d];
 #pragma unroll
-      for (int g = 0; g < NGR - PD; ++g) {
+      for (int g = 0; g < NMG; ++g) {
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq)
           if ((qq * NR) / NS == g) s1c[qq] = OJX_SK_S(sb, 1, qq);
         rr[(g + PD) % XR] = OJX_SK_R(sb, g + PD);
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq) OJX_SK_MFMA(qq, g % NR, g < NR ? s0c[qq] : s1c[qq], rr[g % XR]);
+        if constexpr (DPG > 0)
+          if (g < NDG) OJX_SK_DMA((t + 1) & 1, kn, H0 + g * DPG, min(GPW, H0 + (g + 1) * DPG));
       }
-      sk_sched<0, NGR - PD, NS, NR>();
+      sk_sched<0, NMG, NS, NR, DPG, NDG>();
       if (t + 1 < nk) {
         wait_vmcnt<0>();  // this wave's DMA of stage t+1 has landed
         dma_barrier();    // every wave's has, and every wave's reads of stage t are done
-        if (t + 2 < nk && !(p.dbg & 1)) OJX_SK_DMA(t & 1, kb + (t + 2) * BK);
+        if (t + 2 < nk && !(p.dbg & 1)) OJX_SK_DMA(t & 1, kb + (t + 2) * BK, 0, H0);
         const uint8_t* sx = smem + ((t + 1) & 1) * STAGE;
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq) s0c[qq] = OJX_SK_S(sx, 0, qq);
@@ -235,6 +250,7 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq) OJX_SK_MFMA(qq, g % NR, s1c[qq], rr[g % XR]);
     }
+    wait_vmcnt<0>();  // the last stage's zero-fill DMAs, before LDS is reused
     dma_barrier();  // the next segment's first DMAs reuse buffer 0
 #undef OJX_SK_FRAG
 #undef OJX_SK_S
