@@ -885,6 +885,7 @@ static const TileEntry kTiles[] = {
     OJX_SK(4, 6, 4, 2),             // 76 256 x 192
     OJX_SK(4, 3, 4, 2),             // 77 256 x 96
     OJX_SK(2, 9, 4, 2),             // 78 128 x 288
+    OJX_SK(3, 9, 4, 2),             // 79 192 x 288: 182 W tiles at M <= 288, one round on 256 CUs
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

@@ -391,4 +391,6 @@ template __global__ void gemm_sk_kernel<4, 3, 4, 2>(const GemmParams, const int)
 template __global__ void gemm_sk_fixup_kernel<4, 3, 4, 2>(const GemmParams, const int);
 template __global__ void gemm_sk_kernel<2, 9, 4, 2>(const GemmParams, const int);  // 128 x 288
 template __global__ void gemm_sk_fixup_kernel<2, 9, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_kernel<3, 9, 4, 2>(const GemmParams, const int);  // 192 x 288
+template __global__ void gemm_sk_fixup_kernel<3, 9, 4, 2>(const GemmParams, const int);
 }  // namespace ojx
