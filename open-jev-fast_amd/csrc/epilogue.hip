@@ -19,6 +19,35 @@ namespace ojx {
 
 __device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
 
+// a[v] = sum over the S planes of the float4 at src + 4 v, added in ascending plane order. The loads go out eight
+// planes at a time (indices clamped, extra planes not added) so that S planes cost about S/8 memory latencies
+// rather than S: the reduction runs on few workgroups at small M, where latency is all there is.
+template <int V>
+__device__ __forceinline__ void sum_planes(const float* src, int S, int64_t ps, float4 (&a)[V]) {
+#pragma unroll
+  for (int v = 0; v < V; ++v) a[v] = *reinterpret_cast<const float4*>(src + 4 * v);
+  for (int s0 = 1; s0 < S; s0 += 8) {
+    float4 c[8][V];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t s = s0 + u < S ? s0 + u : S - 1;
+#pragma unroll
+      for (int v = 0; v < V; ++v) c[u][v] = *reinterpret_cast<const float4*>(src + s * ps + 4 * v);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const bool on = s0 + u < S;  // a select, not a branch: the loads above stay one batch
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        a[v].x = on ? a[v].x + c[u][v].x : a[v].x;
+        a[v].y = on ? a[v].y + c[u][v].y : a[v].y;
+        a[v].z = on ? a[v].z + c[u][v].z : a[v].z;
+        a[v].w = on ? a[v].w + c[u][v].w : a[v].w;
+      }
+    }
+  }
+}
+
 __global__ void __launch_bounds__(256) reduce_bf16_k(const float* __restrict__ parts, int S, int64_t ps,
                                                      uint16_t* __restrict__ y, int64_t ldy, int M, int N) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -26,11 +55,9 @@ __global__ void __launch_bounds__(256) reduce_bf16_k(const float* __restrict__ p
   if (idx >= (int64_t)M * n4) return;
   const int m = (int)(idx / n4), n = (int)(idx - (int64_t)m * n4) * 4;
   const float* src = parts + (int64_t)m * N + n;
-  float4 s = *reinterpret_cast<const float4*>(src);
-  for (int k = 1; k < S; ++k) {
-    const float4 t = *reinterpret_cast<const float4*>(src + k * ps);
-    s.x += t.x; s.y += t.y; s.z += t.z; s.w += t.w;
-  }
+  float4 sv[1];
+  sum_planes<1>(src, S, ps, sv);
+  const float4 s = sv[0];
   *reinterpret_cast<uint2*>(y + (int64_t)m * ldy + n) = make_uint2(pack2(s.x, s.y), pack2(s.z, s.w));
 }
 
@@ -42,14 +69,9 @@ __global__ void __launch_bounds__(256) reduce_silu_k(const float* __restrict__ p
   if (idx >= (int64_t)M * nb) return;
   const int m = (int)(idx / nb), blk = (int)(idx - (int64_t)m * nb);
   const float* src = parts + (int64_t)m * N + blk * 8;
-  float4 g = *reinterpret_cast<const float4*>(src);
-  float4 u = *reinterpret_cast<const float4*>(src + 4);
-  for (int k = 1; k < S; ++k) {
-    const float4 a = *reinterpret_cast<const float4*>(src + k * ps);
-    const float4 c = *reinterpret_cast<const float4*>(src + k * ps + 4);
-    g.x += a.x; g.y += a.y; g.z += a.z; g.w += a.w;
-    u.x += c.x; u.y += c.y; u.z += c.z; u.w += c.w;
-  }
+  float4 gu[2];
+  sum_planes<2>(src, S, ps, gu);
+  const float4 g = gu[0], u = gu[1];
   const float o0 = rbf(silu_f(rbf(g.x))) * rbf(u.x), o1 = rbf(silu_f(rbf(g.y))) * rbf(u.y);
   const float o2 = rbf(silu_f(rbf(g.z))) * rbf(u.z), o3 = rbf(silu_f(rbf(g.w))) * rbf(u.w);
   *reinterpret_cast<uint2*>(out + (int64_t)m * ldo + blk * 4) = make_uint2(pack2(o0, o1), pack2(o2, o3));
@@ -68,6 +90,10 @@ __device__ __forceinline__ float block_sum(float v, float* red) {
 }
 
 // One workgroup per row, H/8 threads, 8 contiguous elements per thread.
+// MODE 0: h = x (no add); 1: h = bf16(x + delta); 2: h = bf16(x + bf16(sum of the S fp32 planes)). HN: write hn.
+// Both are template parameters so that each variant is straight-line code and its loads (planes, x, w1) go out
+// together; the split-K variant runs on one workgroup per row, where memory latency is most of its time.
+template <int MODE, bool HN>
 __global__ void __launch_bounds__(1024) add_rmsnorm_k(const uint16_t* __restrict__ x,
                                                       const uint16_t* __restrict__ delta,
                                                       const float* __restrict__ parts, int S, int64_t ps,
@@ -78,53 +104,48 @@ __global__ void __launch_bounds__(1024) add_rmsnorm_k(const uint16_t* __restrict
   __shared__ float red[16];
   const int64_t row = blockIdx.x;
   const int i = threadIdx.x * 8;
+  float d[8];
+  if constexpr (MODE == 2) {
+    float4 ab[2];
+    sum_planes<2>(parts + row * H + i, S, ps, ab);
+    d[0] = rbf(ab[0].x); d[1] = rbf(ab[0].y); d[2] = rbf(ab[0].z); d[3] = rbf(ab[0].w);
+    d[4] = rbf(ab[1].x); d[5] = rbf(ab[1].y); d[6] = rbf(ab[1].z); d[7] = rbf(ab[1].w);
+  } else if constexpr (MODE == 1) {
+    const uint4 da = *reinterpret_cast<const uint4*>(delta + row * H + i);
+    const uint32_t dw[4] = {da.x, da.y, da.z, da.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) { d[2 * j] = bf2f(dw[j] & 0xffffu); d[2 * j + 1] = bf2f(dw[j] >> 16); }
+  }
   const uint4 xa = *reinterpret_cast<const uint4*>(x + row * H + i);
+  float4 wa = make_float4(0.f, 0.f, 0.f, 0.f), wb = wa;
+  if constexpr (HN) {
+    wa = *reinterpret_cast<const float4*>(w1 + i);
+    wb = *reinterpret_cast<const float4*>(w1 + i + 4);
+  }
   const uint32_t xw[4] = {xa.x, xa.y, xa.z, xa.w};
-  float xv[8];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) { xv[2 * j] = bf2f(xw[j] & 0xffffu); xv[2 * j + 1] = bf2f(xw[j] >> 16); }
   float v[8];
-  if (parts != nullptr || delta != nullptr) {
-    float d[8];
-    if (parts != nullptr) {
-      const float* pp = parts + row * H + i;
-      float4 a = *reinterpret_cast<const float4*>(pp), b = *reinterpret_cast<const float4*>(pp + 4);
-      for (int s = 1; s < S; ++s) {
-        const float4 c = *reinterpret_cast<const float4*>(pp + s * ps);
-        const float4 e = *reinterpret_cast<const float4*>(pp + s * ps + 4);
-        a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
-        b.x += e.x; b.y += e.y; b.z += e.z; b.w += e.w;
-      }
-      d[0] = rbf(a.x); d[1] = rbf(a.y); d[2] = rbf(a.z); d[3] = rbf(a.w);
-      d[4] = rbf(b.x); d[5] = rbf(b.y); d[6] = rbf(b.z); d[7] = rbf(b.w);
-    } else {
-      const uint4 da = *reinterpret_cast<const uint4*>(delta + row * H + i);
-      const uint32_t dw[4] = {da.x, da.y, da.z, da.w};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) { d[2 * j] = bf2f(dw[j] & 0xffffu); d[2 * j + 1] = bf2f(dw[j] >> 16); }
-    }
+  for (int j = 0; j < 4; ++j) { v[2 * j] = bf2f(xw[j] & 0xffffu); v[2 * j + 1] = bf2f(xw[j] >> 16); }
+  if constexpr (MODE != 0) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = rbf(xv[j] + d[j]);
+    for (int j = 0; j < 8; ++j) v[j] = rbf(v[j] + d[j]);
     *reinterpret_cast<uint4*>(h_out + row * H + i) =
         make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) v[j] = xv[j];
   }
-  if (hn_out == nullptr) return;  // uniform across the workgroup
-  const float4 wa = *reinterpret_cast<const float4*>(w1 + i), wb = *reinterpret_cast<const float4*>(w1 + i + 4);
-  const bool keep = rowmask == nullptr || rowmask[row] != 0;
-  float ss = 0.f;
+  if constexpr (HN) {
+    const bool keep = rowmask == nullptr || rowmask[row] != 0;
+    float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
-  ss = block_sum(ss, red);
-  const float r = rsqrtf(ss / (float)H + eps);
-  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-  float o[8];
+    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+    ss = block_sum(ss, red);
+    const float r = rsqrtf(ss / (float)H + eps);
+    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+    float o[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) o[j] = keep ? (v[j] * r) * wv[j] : 0.f;
-  *reinterpret_cast<uint4*>(hn_out + row * H + i) =
-      make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+    for (int j = 0; j < 8; ++j) o[j] = keep ? (v[j] * r) * wv[j] : 0.f;
+    *reinterpret_cast<uint4*>(hn_out + row * H + i) =
+        make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+  }
 }
 
 __global__ void __launch_bounds__(256) silu_mul_k(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ tab,
@@ -231,8 +252,15 @@ hipError_t launch_reduce_silu(const float* parts, int S, int64_t ps, uint16_t* o
 hipError_t launch_add_rmsnorm(const uint16_t* x, const uint16_t* delta, const float* parts, int S, int64_t ps,
                               const float* w1, const int32_t* rowmask, float eps, uint16_t* h_out,
                               uint16_t* hn_out, int M, int H, hipStream_t st) {
-  hipLaunchKernelGGL(add_rmsnorm_k, dim3(M), dim3(H / 8), 0, st, x, delta, parts, S, ps, w1, rowmask, eps, h_out,
-                     hn_out, H);
+  const int mode = parts != nullptr ? 2 : delta != nullptr ? 1 : 0;
+  const bool hn = hn_out != nullptr;
+#define OJX_RMS(MO, HV) \
+  hipLaunchKernelGGL((add_rmsnorm_k<MO, HV>), dim3(M), dim3(H / 8), 0, st, x, delta, parts, S, ps, w1, rowmask, eps, \
+                     h_out, hn_out, H)
+  if (mode == 2) { if (hn) OJX_RMS(2, true); else OJX_RMS(2, false); }
+  else if (mode == 1) { if (hn) OJX_RMS(1, true); else OJX_RMS(1, false); }
+  else OJX_RMS(0, true);  // the host never asks for neither output
+#undef OJX_RMS
   return hipGetLastError();
 }
 
