@@ -362,6 +362,32 @@ def test_stream_k_epilogues_and_graph(pkg, ext, O, dev):
         assert torch.equal(junk, eager)
 
 
+@pytest.mark.parametrize("M", [7, 300])
+def test_stream_k_epilogues_ragged_m(pkg, ext, O, dev, M):
+    """The persistent family's epilogues (staged through LDS, one pass per group of fragment columns) on row counts
+    that leave a partial x tile: rows past M must be neither written nor counted in the RMSNorm."""
+    I, K, N = 520, 384, 776
+    g = torch.Generator().manual_seed(M + 5)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
+    wd = (torch.randn(N, K, generator=g) * 0.01).bfloat16()
+    res = torch.randn(M, N, generator=g).bfloat16()
+    w1 = (1.0 + 0.1 * torch.randn(N, generator=g)).float()
+    ref_silu = O.gate_up_silu(x, wg, wu)
+    rh, rhn = O.residual_proj(res, x, wd, w1, None, 1e-6, S=1)
+    xd, packed = x.to(dev), ext.pack_gate_up(wg.to(dev), wu.to(dev))
+    for t in _sk_tiles(pkg):
+        for S in (1, 2):
+            _say(f"case stream-K ragged M={M} tile={t} S={S}")
+            out = ext.mm_silu_mul(xd, packed, cfg=(t, S))
+            assert out.shape == (M, I)
+            _assert_tol(O, out, ref_silu, f"silu M {M} tile {t} S {S}")
+            h, hn = ext.mm_residual_rmsnorm(res.to(dev), xd, wd.to(dev), w1.to(dev), None, 1e-6, cfg=(t, S))
+            _assert_tol(O, h, rh, f"h M {M} tile {t} S {S}")
+            _assert_tol(O, hn, rhn, f"hn M {M} tile {t} S {S}")
+
+
 # ----------------------------------------------------------------------------------------------- scoring head
 @pytest.mark.parametrize("R", [1, 7, 64, 539])
 def test_head_scores_vs_oracle(pkg, ext, O, dev, R):
