@@ -1,7 +1,7 @@
 """Runs one projection configuration repeatedly, for rocprofv3 (kernel traces and --pmc counter passes).
 
-    rocprofv3 --kernel-trace --stats -d gpurun_out/prof -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
-    rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
+    rocprofv3 --kernel-trace --stats -d /tmp/prof -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
+    rocprofv3 --pmc FETCH_SIZE -d /tmp/pmc -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
     python3 open-jev-fast_amd/prof.py --copy-mb 512     # plain copy kernel, to calibrate FETCH_SIZE / WRITE_SIZE
 
 Shapes are those of open_jev_fast_amd.perf.SHAPES (plus any --n/--k override); weights rotate over copies larger

@@ -3,7 +3,7 @@ plan table (csrc/plan_table.inc) that ojx_plan() reads. Replaces the reference's
 (_tune src/fastmodel.py:114-132, bench/lt_search.py) with a one-time offline sweep, so nothing is timed at run
 time or during graph capture.
 
-    python open-jev-fast_amd/tune.py --out gpurun_out/plan_table.inc [--m 7,288] [--shapes gate_up,down]
+    python open-jev-fast_amd/tune.py --out /tmp/plan_table.inc [--m 7,288] [--shapes gate_up,down]
 
 Each candidate is timed by graph replay over rotating weight copies (larger than the Infinity Cache); the winner
 is checked against a torch fp32 GEMM on the GPU before it is accepted (max rel 1e-2, mean |d| <= 1e-3 RMS).
