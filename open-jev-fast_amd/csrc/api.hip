@@ -207,11 +207,6 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.sk_cnt = nullptr;
   p.dp_tiles = 0;
   p.sk_grid = 0;
-  {
-    static int dbg = -1;
-    if (dbg < 0) { const char* e = getenv("OJX_DEBUG"); dbg = e ? atoi(e) : 0; }
-    p.dbg = dbg;
-  }
   int grid = 0;
   if (t->family == 5) {
     const SkPlan sp = sk_plan(t, M, N, K, c.splitk);

@@ -161,7 +161,7 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     // ------------------------------------------------------------------ main loop
 #define OJX_SK_DMA(buf, k0, lo, hi)                                                                        \
   do {                                                                                                     \
-    const uint32_t kof_ = (p.dbg & 2) ? 0u : (uint32_t)(k0) * 2u;                                          \
+    const uint32_t kof_ = (uint32_t)(k0) * 2u;                                                             \
     /* keep the per-block offsets as one multiply-add each instead of GPW registers held across the loop */ \
     asm volatile("" : "+s"(stepW), "+s"(stepX));                                                           \
     _Pragma("unroll") for (int i = (lo); i < (hi); ++i) {                                                  \
@@ -238,7 +238,7 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       if (t + 1 < nk) {
         wait_vmcnt<0>();  // this wave's DMA of stage t+1 has landed
         dma_barrier();    // every wave's has, and every wave's reads of stage t are done
-        if (t + 2 < nk && !(p.dbg & 1)) OJX_SK_DMA(t & 1, kb + (t + 2) * BK, 0, H0);
+        if (t + 2 < nk) OJX_SK_DMA(t & 1, kb + (t + 2) * BK, 0, H0);
         const uint8_t* sx = smem + ((t + 1) & 1) * STAGE;
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq) s0c[qq] = OJX_SK_S(sx, 0, qq);

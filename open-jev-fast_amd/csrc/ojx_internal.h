@@ -48,7 +48,6 @@ struct GemmParams {
   uint32_t* sk_cnt;                 // arrival counter per stream-K tile: zero on entry, left zero on exit
   int dp_tiles;                     // tiles done whole first (a multiple of the grid)
   int sk_grid;                      // workgroups that share the remaining tiles' K iterations
-  int dbg;                          // experiment switches (0 in production)
 };
 
 struct TileInfo {
