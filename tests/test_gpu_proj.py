@@ -3,6 +3,7 @@
 Tolerance: max |out - ref| / max |ref| <= 1e-2 and mean |out - ref| <= 1e-3 * RMS(ref).
 Integer-like invariants (gate/up merge, tile invariance, determinism, graph replays) are checked bit-exactly.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -386,6 +387,36 @@ def test_stream_k_epilogues_ragged_m(pkg, ext, O, dev, M):
             h, hn = ext.mm_residual_rmsnorm(res.to(dev), xd, wd.to(dev), w1.to(dev), None, 1e-6, cfg=(t, S))
             _assert_tol(O, h, rh, f"h M {M} tile {t} S {S}")
             _assert_tol(O, hn, rhn, f"hn M {M} tile {t} S {S}")
+
+
+def test_bf16_rounding_bit_patterns(ext, dev):
+    """Every fp32 -> bf16 rounding in the kernels (one hardware conversion) is round-to-nearest-even, checked
+    bit-exactly against torch's CPU conversion on about a million fp32 bit patterns: random words, the three
+    patterns around every tie of random bf16 values, denormals, the largest finite values (and the ones that
+    round to inf), infinities and NaNs. They go through the split-K RMSNorm with S = 1 and x = 0, whose h is
+    bf16(0 + bf16(plane)), i.e. the rounding itself (a -0 result becomes +0)."""
+    H = 5120
+    rng = np.random.default_rng(7)
+    rand = rng.integers(0, 2 ** 32, size=150 * H, dtype=np.uint64).astype(np.uint32)
+    hi = rng.integers(0, 2 ** 16, size=16 * H, dtype=np.uint64).astype(np.uint32) << 16
+    ties = np.concatenate([hi | 0x7FFF, hi | 0x8000, hi | 0x8001])
+    special = np.array([0, 0x80000000, 1, 0x8000, 0x7FFFFF, 0x807FFFFF, 0x00800000, 0x7F7FFFFF, 0x7F7F8000,
+                        0x7F7F7FFF, 0xFF7FFFFF, 0xFF7F8000, 0x7F800000, 0xFF800000, 0x7FC00000, 0x7F800001,
+                        0xFFFFFFFF, 0x3F808000, 0x3F818000], dtype=np.uint32)
+    pat = np.concatenate([rand, ties, special])
+    pat = np.concatenate([pat, np.zeros((-len(pat)) % H, dtype=np.uint32)])
+    M = len(pat) // H
+    vals = torch.from_numpy(pat.view(np.float32).copy()).reshape(M, H)
+    _say(f"case bf16 rounding patterns M={M} H={H}")
+    x = torch.zeros(M, H, dtype=torch.bfloat16, device=dev)
+    h, _ = ext.add_rmsnorm_sk(x, vals.reshape(1, M, H).to(dev), torch.ones(H, device=dev), None, 1e-6)
+    got = h.cpu().view(torch.int16).numpy().view(np.uint16)
+    ref = vals.to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16).copy()
+    ref[ref == 0x8000] = 0
+    nan = np.isnan(vals.numpy())
+    assert np.all(((got & 0x7FFF) > 0x7F80)[nan]), "NaN must stay NaN"
+    bad = np.flatnonzero((got != ref) & ~nan)
+    assert bad.size == 0, f"{bad.size} roundings differ, first input 0x{pat[bad[0]]:08x}: 0x{got.flat[bad[0]]:04x} vs 0x{ref.flat[bad[0]]:04x}"
 
 
 # ----------------------------------------------------------------------------------------------- scoring head
