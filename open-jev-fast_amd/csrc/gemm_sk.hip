@@ -13,9 +13,14 @@
 //     wave instruction) in stages of 64 k, two LDS buffers: stage t+1 is in flight while stage t is multiplied, and
 //     no registers are spent on staging. LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row / 2) mod
 //     8, so the 16 rows that one ds_read_b128 touches land on 16 distinct bank groups. (Stages of 32 k with four
-//     buffers were measured slower: twice the barriers, and no gain from the deeper DMA queue.)
+//     buffers were measured slower: twice the barriers, and no gain from the deeper DMA queue.) Half of a stage's
+//     DMA instructions go out after the barrier that frees their buffer, the rest one per MFMA group of the next
+//     stage: issued in one burst they fill the texture unit's command queue and stall the issuing waves.
 //   * The operand with fewer fragments per wave stays in registers for a stage; the other one's fragments are read
 //     two MFMA groups ahead, so LDS latency hides behind MFMAs.
+//   * The body is compiled once per epilogue mode. The epilogue stages the accumulators through LDS a few fragment
+//     columns at a time and applies the mode in a short rolled loop (the fully unrolled form was instruction-fetch
+//     bound); its SiLU arithmetic is what remains of its cost.
 //   * Persistent grid of one workgroup per CU. Tiles are first handed out in whole-tile waves of G (one tile per
 //     workgroup, XCD-aware order so that the M tiles of one W tile run on the same XCD at the same time and share
 //     its L2). The tiles left over (fewer than G) would leave most CUs idle for a whole tile time; instead their
