@@ -927,7 +927,8 @@ hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t strea
   err = hipGetLastError();
   if (err != hipSuccess || e.fixup == nullptr || p.sk_ws == nullptr) return err;
   const int rem = p.tiles_n * p.tiles_m - p.dp_tiles;  // the stream-K tiles
-  hipLaunchKernelGGL(e.fixup, dim3(rem), dim3(e.info.threads), 0, stream, p, epi);
+  const int fn = e.info.bn / (16 * e.info.wn);          // one workgroup per tile and fragment column
+  hipLaunchKernelGGL(e.fixup, dim3(rem * fn), dim3(e.info.threads), 0, stream, p, epi);
   return hipGetLastError();
 }
 

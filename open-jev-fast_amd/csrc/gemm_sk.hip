@@ -345,9 +345,11 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
   else sk_body<FN, FM, WN, WM, EPI_BF16>(p);  // the host routes EPI_F32 (split-K planes) to other families
 }
 
-// Second pass of a stream-K plan, one workgroup per remaining tile (same waves and fragment ownership as the GEMM):
-// a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and applies the epilogue; a tile done
-// whole by one workgroup was finished by the GEMM. The pieces are visible here because the GEMM launch has ended.
+// Second pass of a stream-K plan, one workgroup per remaining tile and fragment column i (same waves and fragment
+// ownership as the GEMM; FN workgroups per tile, since one per tile left this pass bound by the bandwidth of a few
+// dozen CUs): a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and applies the
+// epilogue; a tile done whole by one workgroup was finished by the GEMM. The pieces are visible here because the
+// GEMM launch has ended.
 template <int FN, int FM, int WN, int WM>
 __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmParams p, const int epi) {
   constexpr int BN = WN * FN * 16, BM = WM * FM * 16, BK = 64, FRAG = 256;
@@ -356,7 +358,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmP
   const int wn = wave % WN, wm = wave / WN;
   const int lr = lane & 15, lg = lane >> 4;
   const int ipt = (p.K + BK - 1) / BK;
-  const int ts = blockIdx.x;
+  const int ts = blockIdx.x / FN, i = blockIdx.x % FN;
   const int64_t T = (int64_t)(p.tiles_n * p.tiles_m - p.dp_tiles) * ipt;
   const int64_t Gs = p.sk_grid;
   const int64_t x0 = (int64_t)ts * ipt;
@@ -371,13 +373,20 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmP
   const int tau = p.dp_tiles + ts;
   const int n0 = (tau / p.tiles_m) * BN, m0 = (tau % p.tiles_m) * BM;
   const float* base = p.sk_ws + (int64_t)wave * FN * FM * FRAG + lane * 4;
-  for (int i = 0; i < FN; ++i)
-    for (int j = 0; j < FM; ++j) {
-      const float* src = base + (i * FM + j) * FRAG;
-      f32x4 v = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[0] * (BN * BM));
-      for (int k = 1; k < np; ++k) v += *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[k] * (BN * BM));
-      store_tile(p, epi, 0, m0 + (wm * FM + j) * 16 + lr, n0 + (wn * FN + i) * 16 + lg * 4, lg, v);
-    }
+  const float* src = base + i * FM * FRAG;
+  f32x4 v[FM];
+#pragma unroll
+  for (int j = 0; j < FM; ++j) v[j] = *reinterpret_cast<const f32x4*>(src + j * FRAG + (int64_t)s_slot[0] * (BN * BM));
+  for (int k = 1; k < np; ++k) {  // the FM loads of one piece are in flight together
+    f32x4 c[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) c[j] = *reinterpret_cast<const f32x4*>(src + j * FRAG + (int64_t)s_slot[k] * (BN * BM));
+#pragma unroll
+    for (int j = 0; j < FM; ++j) v[j] += c[j];
+  }
+#pragma unroll
+  for (int j = 0; j < FM; ++j)
+    store_tile(p, epi, 0, m0 + (wm * FM + j) * 16 + lr, n0 + (wn * FN + i) * 16 + lg * 4, lg, v[j]);
 }
 
 }  // namespace ojx
