@@ -50,7 +50,7 @@ def main():
     ap.add_argument("--max-waves", type=float, default=16.0, help="skip candidates with more workgroups than this "
                     "many per CU")
     ap.add_argument("--no-tails", action="store_true", help="simple (tile, split-K) candidates only")
-    ap.add_argument("--sk-splits", default="1,2,4,8", help="stream-K spreads tried for the persistent family")
+    ap.add_argument("--sk-splits", default="1,2,3,4,6,8", help="stream-K spreads tried for the persistent family")
     args = ap.parse_args()
     Ms = [int(m) for m in args.m.split(",")] if args.m else list(M_DEFAULT)
     sk_splits = {int(v) for v in args.sk_splits.split(",")}
