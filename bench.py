@@ -11,7 +11,8 @@ CPU baseline (the oracle's torch CPU path on a bounded sample of the same worklo
 per-shape table at M = 7 / 288 / 539 for the five projection shapes.
 
 Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
-the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV).
+the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV), --vs-hipblaslt
+(each planned call against torch F.linear on the same box).
 """
 import argparse
 import json
@@ -295,6 +296,35 @@ def main_head(args, pkg, ext, perf):
                           "frac": round(nbytes / perf.HBM_PEAK / t, 4)}), flush=True)
 
 
+def main_vs_hipblaslt(args, pkg, ext, perf):
+    """This build's planned call against torch F.linear (hipBLASLt) on the same box, in one process: each timed as a
+    HIP graph of 10 calls over the same rotating weight copies (perf.gpu_time), best of two measurements. The ojx
+    call includes its fused epilogue (SiLU.mul, or residual + RMSNorm); the hipBLASLt time is the GEMM alone."""
+    dev = "cuda"
+    Ms = [int(m) for m in args.m.split(",")] if args.m else [7, 288, 539, 1024, 2048]
+    names = args.shapes.split(",") if args.shapes else list(perf.SHAPES)
+    for name in names:
+        N, K, kind = perf.SHAPES[name]
+        ws = [(torch.randn(N, K, device=dev) * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+        for M in Ms:
+            x = torch.randn(M, K, device=dev).bfloat16()
+            res = torch.randn(M, N, device=dev).bfloat16()
+            w1 = torch.ones(N, device=dev)
+            blas = [lambda w=w: torch.nn.functional.linear(x, w) for w in ws]
+            if kind == "plain":
+                ours = [lambda w=w: ext.mm(x, w) for w in ws]
+            elif kind == "silu":
+                ours = [lambda w=w: ext.mm_silu_mul(x, w) for w in ws]
+            else:
+                ours = [lambda w=w: ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6) for w in ws]
+            t_b = min(perf.gpu_time(blas, iters=10, reps=3), perf.gpu_time(blas, iters=10, reps=3))
+            t_o = min(perf.gpu_time(ours, iters=10, reps=3), perf.gpu_time(ours, iters=10, reps=3))
+            print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "epilogue": kind, "ojx_us": round(t_o * 1e6, 1),
+                              "hipblaslt_gemm_us": round(t_b * 1e6, 1), "ratio": round(t_b / t_o, 3)}), flush=True)
+        del ws
+        torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -303,6 +333,7 @@ def main():
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--stack", action="store_true")
     ap.add_argument("--head", action="store_true")
+    ap.add_argument("--vs-hipblaslt", action="store_true")
     ap.add_argument("--m", default="")
     ap.add_argument("--shapes", default="")
     ap.add_argument("--no-cpu", action="store_true")
@@ -323,6 +354,8 @@ def main():
         main_stack(args, pkg, ext, perf)
     elif args.head:
         main_head(args, pkg, ext, perf)
+    elif args.vs_hipblaslt:
+        main_vs_hipblaslt(args, pkg, ext, perf)
     else:
         main_default(args, pkg, ext, perf)
 
