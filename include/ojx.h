@@ -9,9 +9,8 @@
  * Every entry point returns OJX_OK (0) or an error code; ojx_last_error() gives the message of the last failure
  * on the calling thread. Launches go on the given stream, never synchronize and never allocate, so they can be
  * captured into a HIP graph. Entry points that take a workspace need ojx_workspace_bytes() bytes of device memory
- * there (0 bytes when the plan has no split-K and no stream-K partial tiles). The first 4096 bytes of a workspace
- * are reserved for arrival counters: keep them zero (allocate the workspace zero-filled once and reuse it); calls
- * leave them zero. The rest is scratch for one call.
+ * there (0 bytes when the plan has no split-K and no stream-K partial tiles). A workspace is scratch for one call:
+ * its contents on entry do not matter, and two calls that may run at the same time need separate workspaces.
  *
  * Global state (the plan table, kernel attributes) is read-only after the first call; concurrent calls on
  * different streams are safe as long as they do not share output or workspace buffers.
@@ -56,6 +55,7 @@ typedef struct {
 } ojx_cfg;
 
 const char* ojx_last_error(void);
+/* "ojx <version> gfx950 src:<digest>": the digest hashes the sources the library was built from. */
 const char* ojx_version(void);
 
 /* Sets kernel attributes on the current device. Optional: every launch does it on first use. */

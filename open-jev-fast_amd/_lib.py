@@ -70,8 +70,21 @@ def lib():
             f = getattr(L, name)
             f.restype = res
             f.argtypes = args
+        _check_provenance(L)
         _lib = L
     return _lib
+
+
+def _check_provenance(L) -> None:
+    """The library must have been compiled from the sources beside it: ojx_version() carries a digest of csrc/ and
+    include/ojx.h taken at build time. A stale build (sources edited, library not rebuilt) raises, so tests and
+    benchmarks never run a binary other than the one the tree describes. OJX_ALLOW_STALE=1 skips the check."""
+    from .build import source_digest
+    got = L.ojx_version().decode()
+    want = source_digest()
+    if not got.endswith("src:" + want) and os.environ.get("OJX_ALLOW_STALE") != "1":
+        raise RuntimeError(f"{LIB_PATH} ({got}) was not built from these sources (digest {want}): rebuild it with "
+                           "__graft_entry__.build() or python open-jev-fast_amd/build.py")
 
 
 def check(rc: int) -> None:

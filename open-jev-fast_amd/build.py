@@ -3,6 +3,7 @@
 Run as `python open-jev-fast_amd/build.py` or through `__graft_entry__.build()`. The library lands next to this file
 so that it travels with the source tree; nothing is installed.
 """
+import hashlib
 import os
 import subprocess
 import sys
@@ -26,15 +27,35 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
          f"-I{INCLUDE}", f"-I{CSRC}"]
 
 
+def source_files():
+    """Every file the library is compiled from: csrc/ (kernels, C-ABI, plan table) and include/ojx.h."""
+    files = [os.path.join(CSRC, f) for f in sorted(os.listdir(CSRC))
+             if f.endswith((".hip", ".h", ".inc"))]
+    return files + [os.path.join(INCLUDE, "ojx.h")]
+
+
+def source_digest() -> str:
+    """sha256 (first 16 hex digits) over the names and bytes of source_files(). It is compiled into the library
+    (ojx_version() ends in "src:<digest>"), so a loaded libojx.so can be checked against the tree beside it."""
+    h = hashlib.sha256()
+    for f in source_files():
+        h.update(os.path.basename(f).encode() + b"\0")
+        with open(f, "rb") as fh:
+            h.update(fh.read())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
+
+
 def build(verbose: bool = False) -> str:
     """Compiles every source into libojx.so (always rebuilds; the translation units compile in parallel).
     Returns the library path."""
     os.makedirs(OBJDIR, exist_ok=True)
     noise = "is not a recognized feature for this target"
     jobs = []
+    digest = source_digest()
     for s in SOURCES:
         obj = os.path.join(OBJDIR, s.replace(".hip", ".o"))
-        cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, s), "-o", obj]
+        cmd = [HIPCC, *FLAGS, f'-DOJX_SRC_DIGEST="{digest}"', "-c", os.path.join(CSRC, s), "-o", obj]
         jobs.append((cmd, obj, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
     errs = []
     for cmd, obj, pr in jobs:

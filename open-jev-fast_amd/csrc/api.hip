@@ -46,11 +46,7 @@ constexpr int kSplits[] = {1, 2, 3, 4, 5, 6, 8, 10, 12, 16};
 constexpr int kMaxSplit = 16;
 
 constexpr int kSkMaxPieces = 64;  // gemm_sk.hip: pieces one stream-K tile may be split into
-// Every workspace starts with this many bytes of stream-K arrival counters (one per remainder tile, fewer than the
-// grid): zero before the first call, left zero by every call. The launch data (partial tiles, split-K planes)
-// follows, so no layout ever writes over the counters.
-constexpr int64_t kCntBytes = 4096;
-constexpr int kMaxGrid = (int)(kCntBytes / 4);
+constexpr int kMaxGrid = 1024;    // persistent grid cap (one workgroup per CU)
 
 bool is_sk(int32_t tile) {
   const ojx::TileInfo* t = ojx::tile_info(tile);
@@ -74,7 +70,7 @@ int device_cus() {
 // then the K iterations of the remaining R tiles shared by gs workgroups (at most S pieces per tile on average).
 struct SkPlan {
   int grid, dp, gs;
-  bool partial;        // some tile is split over several workgroups: counters and partial slots are used
+  bool partial;        // some tile is split over several workgroups: partial slots are used
   int64_t slot_bytes;  // 2 gs partial tiles of fp32
 };
 SkPlan sk_plan(const ojx::TileInfo* t, int64_t M, int64_t N, int64_t K, int32_t S) {
@@ -118,7 +114,7 @@ struct Part {
   int64_t n0, n; // W rows (output columns) it covers
   int64_t ws;    // byte offset of its split-K partials in the workspace
 };
-// Workspace of one launch: the stream-K counters and partial slots, or the split-K fp32 planes.
+// Workspace of one launch: the stream-K partial slots, or the split-K fp32 planes.
 int64_t part_ws_bytes(const ojx_cfg& c, int64_t M, int64_t n, int64_t K) {
   if (is_sk(c.tile)) {
     const SkPlan sp = sk_plan(ojx::tile_info(c.tile), M, n, K, c.splitk);
@@ -128,18 +124,16 @@ int64_t part_ws_bytes(const ojx_cfg& c, int64_t M, int64_t n, int64_t K) {
 }
 int split_parts(const ojx_cfg& c, int64_t M, int64_t N, int64_t K, Part out[2]) {
   const int64_t nt = c.tail_rows;
-  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, kCntBytes};
+  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, 0};
   if (nt == 0) return 1;
-  const int64_t ws0 = kCntBytes + part_ws_bytes(out[0].c, M, N - nt, K);
+  const int64_t ws0 = cdiv(part_ws_bytes(out[0].c, M, N - nt, K), 256) * 256;
   out[1] = Part{ojx_cfg{c.tail_tile, c.tail_splitk, 0, 1, 0}, N - nt, nt, ws0};
   return 2;
 }
 int64_t workspace_for(const ojx_cfg& c, int64_t M, int64_t N, int64_t K) {
   Part parts[2];
   const int np = split_parts(c, M, N, K, parts);
-  int64_t total = 0;
-  for (int i = 0; i < np; ++i) total += part_ws_bytes(parts[i].c, M, parts[i].n, K);
-  return total > 0 ? kCntBytes + total : 0;
+  return parts[np - 1].ws + part_ws_bytes(parts[np - 1].c, M, parts[np - 1].n, K);
 }
 
 ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
@@ -204,7 +198,6 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.tiles_m = (int)cdiv(M, t->bm);
   p.splits = c.splitk;
   p.sk_ws = nullptr;
-  p.sk_cnt = nullptr;
   p.dp_tiles = 0;
   p.sk_grid = 0;
   int grid = 0;
@@ -216,7 +209,6 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
     grid = sp.grid;
     if (sp.partial) {
       if (ws == nullptr) return fail(OJX_ERR_WORKSPACE, "stream-K plan needs a workspace");
-      p.sk_cnt = static_cast<uint32_t*>(ws);
       p.sk_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off);
     }
   }
@@ -260,7 +252,12 @@ int check_rows(int64_t M, int64_t H) {
 extern "C" {
 
 const char* ojx_last_error(void) { return g_err.c_str(); }
-const char* ojx_version(void) { return "ojx 0.1 gfx950"; }
+#ifndef OJX_SRC_DIGEST
+#define OJX_SRC_DIGEST "unknown"
+#endif
+// The digest is a hash of the sources the library was compiled from (computed by the package's build script), so a
+// caller can tell whether the loaded binary matches a source tree.
+const char* ojx_version(void) { return "ojx 0.2 gfx950 src:" OJX_SRC_DIGEST; }
 
 int ojx_init(void) { return hip_check(ojx::init_tiles(), "kernel attribute setup"); }
 
@@ -434,14 +431,14 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   uint16_t* hn = static_cast<uint16_t*>(hn_out);
   if (c.splitk == 1 || is_sk(c.tile)) {
     OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
-    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, kCntBytes));
+    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0));
     if (hn == nullptr) return OJX_OK;
     return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,
                                              (int)N, st), "rmsnorm launch");
   }
   if (hn == nullptr && N / 8 > 1024) return fail(OJX_ERR_SHAPE, "split-K residual needs N/8 <= 1024");
   OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
-  float* parts = reinterpret_cast<float*>(static_cast<char*>(workspace) + kCntBytes);
+  float* parts = static_cast<float*>(workspace);
   OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st));
   return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(residual), nullptr, parts, c.splitk, M * N,
                                            w1, rowmask, eps, h, hn, (int)M, (int)N, st), "rmsnorm launch");

@@ -43,7 +43,6 @@ struct GemmParams {
   int tiles_n, tiles_m, splits;
   // persistent stream-K kernels (family 5) only
   float* sk_ws;                     // partial-tile slots, 2 per workgroup, BN*BM fp32 each
-  uint32_t* sk_cnt;                 // arrival counter per stream-K tile: zero on entry, left zero on exit
   int dp_tiles;                     // tiles done whole first (a multiple of the grid)
   int sk_grid;                      // workgroups that share the remaining tiles' K iterations
 };

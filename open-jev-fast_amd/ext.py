@@ -51,16 +51,19 @@ def _cfgp(cfg):
     return ctypes.byref(cfg)
 
 
-_WS = {}
+_WS = {}        # device index -> the workspace handed to eager calls and captures
+_WS_KEEP = []   # every workspace a graph capture has used: kept alive for the life of the process
 
 
 def _workspace(M, N, K, kind, cfg, device):
-    """Workspace of one call: split-K planes, or the stream-K arrival counters and partial slots.
+    """Workspace of one call: split-K fp32 planes or stream-K partial tiles (scratch, contents irrelevant on entry).
 
-    The counters must be zero before a call and every call leaves them zero, so one zero-filled buffer per device
-    is kept and grown as needed (grown outside graph capture). Calls that run concurrently on different streams of
-    one device would share it: such callers use the C-ABI with a workspace of their own. When a graph capture needs
-    more than the kept buffer holds, the capture gets a buffer of its own whose zero fill is recorded with it."""
+    One buffer per device is kept and grown as needed. A graph capture records the buffer's address, so a buffer
+    that a capture has used is never freed: when an eager call later needs a larger one, the old buffer moves to
+    _WS_KEEP instead of going back to the caching allocator (where a replay would write into memory that other
+    tensors may own by then). A capture that needs more than the kept buffer gets a buffer of its own, also kept.
+    Calls that run concurrently on different streams of one device would share the buffer: such callers pass a
+    workspace of their own through the C-ABI."""
     n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
     if n < 0:
         check(1)
@@ -68,13 +71,19 @@ def _workspace(M, N, K, kind, cfg, device):
         return None, 0
     key = torch.device(device).index
     ws = _WS.get(key)
-    if ws is not None and ws.numel() >= n:
-        return ws, ws.numel()
-    if torch.cuda.is_current_stream_capturing():
-        return torch.zeros(n, dtype=torch.uint8, device=device), n
-    ws = torch.zeros(max(n, 1 << 20), dtype=torch.uint8, device=device)
-    _WS[key] = ws
-    return ws, ws.numel()
+    capturing = torch.cuda.is_current_stream_capturing()
+    if ws is not None and ws[0].numel() >= n:
+        if capturing and not ws[1]:
+            _WS[key] = ws = (ws[0], True)
+            _WS_KEEP.append(ws[0])
+        return ws[0], ws[0].numel()
+    if capturing:
+        buf = torch.empty(n, dtype=torch.uint8, device=device)
+        _WS_KEEP.append(buf)
+        return buf, n
+    buf = torch.empty(max(n, 1 << 20), dtype=torch.uint8, device=device)
+    _WS[key] = (buf, False)   # the old buffer, if a capture used it, stays alive in _WS_KEEP
+    return buf, buf.numel()
 
 
 # ------------------------------------------------------------------------------------------------ epilogues

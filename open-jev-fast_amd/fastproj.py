@@ -21,10 +21,28 @@ from . import _lib, ext
 LUT = os.environ.get("OJ_LUT", "1") == "1"
 
 
+_SPLIT_ENV = ("OJ_SK_LIN_OUT", "OJ_SK_FULL_OUT", "OJ_SK_DOWN")
+
+
 def _env_split(name):
     """OJ_SK_* override of the split-K count; unset means the plan table decides."""
     v = os.environ.get(name)
     return int(v) if v else None
+
+
+def _split_forced():
+    """True when the user set one of the reference's split-K variables (src/fastmodel.py:55-57). Only then is the
+    S that the forward passes to _res applied; the reference's __init__ always sets S (default 2,
+    src/fastmodel.py:92,97,109), and on MI355X the measured plan is better than a fixed split."""
+    return any(os.environ.get(n) for n in _SPLIT_ENV)
+
+
+def _wsk_2d(wsk, what):
+    if wsk.dim() != 2:
+        raise RuntimeError(f"{what}: the split-K weight must be W itself, [N, K] (FastProjections._split returns it "
+                           f"unchanged); got shape {tuple(wsk.shape)}, the reference's [S, K/S, N] copy "
+                           "(src/fastmodel.py:186-188), which libojx does not read")
+    return wsk
 
 
 class FastProjections:
@@ -79,11 +97,14 @@ class FastProjections:
         return c
 
     def _tune_sk(self, y, wsk, S):
+        """Tile for the split-K partial GEMM (_skmm): the residual plan's tile when it writes split-K planes, else -1
+        (the library then picks a plane-writing tile itself; the persistent family has no K planes)."""
         M, K = y.shape
-        N = wsk.shape[0]
+        N = _wsk_2d(wsk, "_tune_sk").shape[0]
         c = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
-        self._sk_best[(M, N, K, S)] = c.tile
-        return c.tile
+        tile = c.tile if _lib.tile_info(c.tile)["family"] != 5 else -1
+        self._sk_best[(M, N, K, S)] = tile
+        return tile
 
     # ------------------------------------------------------------------------------------- projections
     def _mm(self, x, w):
@@ -94,8 +115,9 @@ class FastProjections:
         return ext.mm(x, w, cfg=c)
 
     def _skmm(self, y, wsk, S):
+        """parts [S, M, N] fp32 = the S K-chunks of y times W (the reference's torch.bmm / lt2_run)."""
         M, K = y.shape
-        key = (M, wsk.shape[0], K, S)
+        key = (M, _wsk_2d(wsk, "_skmm").shape[0], K, S)
         tile = self._sk_best.get(key)
         if tile is None:
             tile = self._tune_sk(y, wsk, S)
@@ -112,13 +134,26 @@ class FastProjections:
         return ext.mm_silu_mul(x, w_gu_packed)
 
     def _res(self, h, y, wsk, S, w1, mask, w=None):
-        """(h_new, hn) = residual add + RMSNorm after the out / down projection (src/fastmodel.py:196-203).
-        S None / 0 = the plan table's split; an explicit S forces that split with the plan's tile."""
-        W = w if w is not None else wsk
+        """(h_new, hn) = residual add + RMSNorm after the out / down projection (src/fastmodel.py:196-203), as one
+        call of the fused projection. The configuration (tile, split-K or stream-K spread) comes from the plan
+        table. The S the forward passes (the reference's d.sk_out / d.sk_down, 2 by default) is applied only when
+        an OJ_SK_* variable is set, as a split-K count with a tile that writes K planes."""
+        W = w if w is not None else _wsk_2d(wsk, "_res")
         M, K = y.shape
         N = W.shape[0]
         cfg = None
-        if S:
-            c = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
-            cfg = _lib.cfg(c.tile, int(S))
+        if S and _split_forced():
+            cfg = self._forced_cfg(M, N, K, int(S))
         return ext.mm_residual_rmsnorm(h, y, W, w1, mask, self.eps, want_hn=True, cfg=cfg)
+
+    @staticmethod
+    def _forced_cfg(M, N, K, S):
+        """(tile, S) for an explicit split-K count: the plan's tile if it writes K planes, else the first candidate
+        with that split that does. None (the plan) if no candidate takes S for this shape."""
+        plan = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
+        cands = [c for c in _lib.candidates(M, N, K, _lib.KIND_RESIDUAL)
+                 if c.splitk == S and _lib.tile_info(c.tile)["family"] != 5]
+        for c in cands:
+            if c.tile == plan.tile:
+                return c
+        return cands[0] if cands else None

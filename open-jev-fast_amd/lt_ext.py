@@ -9,8 +9,10 @@
     LT.lt2_info(h, idx); LT.lt2_raw(h, idx); LT.lt2_add_raw(h, raw)                 (src/lt.cpp:170-190)
 
 A "candidate" is a (tile, split-K) pair of libojx rather than a cuBLASLt algorithm; a raw descriptor is that pair.
-Differences, on purpose: split-K weights stay [N, K] (wl=0 and wl=1 both take the [N, K] weight, because the kernel
-reads K ranges of W in place), and only fp32 partials exist (f32=0 raises), which is what the reference uses.
+Differences, on purpose: split-K weights stay [N, K]. A plan made with wl=1 (the reference's split-K layout
+[S, K/S, N], src/lt.cpp:58-59) still takes the [N, K] weight in lt2_run, because the kernel reads the K chunks of W
+in place; a 3-D [S, K/S, N] weight raises a RuntimeError that names the layout. Only fp32 partials exist (f32=0
+raises), which is what the reference uses.
 """
 import torch
 
@@ -46,9 +48,13 @@ class _LT:
             raise RuntimeError("only fp32 split-K partials are supported (f32=1)")
         if wl not in (0, 1):
             raise RuntimeError("wl must be 0 or 1")
+        if wl == 0 and int(S) != 1:
+            raise RuntimeError("wl=0 (w [N, K]) needs S == 1")   # the reference's TORCH_CHECK, src/lt.cpp:67
+        # tiles that write split-K planes (the persistent family's splitk is a stream-K spread, with no K planes)
         tiles = sorted({c.tile for c in _lib.candidates(int(M), int(N), int(K), _lib.KIND_RESIDUAL)
-                        if c.splitk == int(S)})
-        self._sk.append({"shape": (int(M), int(N), int(K)), "S": int(S), "tiles": tiles, "found": tiles})
+                        if c.splitk == int(S) and _lib.tile_info(c.tile)["family"] != 5})
+        self._sk.append({"shape": (int(M), int(N), int(K)), "S": int(S), "wl": int(wl), "tiles": tiles,
+                         "found": tiles})
         return len(self._sk) - 1
 
     def _plan(self, h):
@@ -66,6 +72,10 @@ class _LT:
         if not 0 <= idx < len(p["found"]):
             raise RuntimeError(f"candidate index {idx} out of range [0, {len(p['found'])})")
         M, N, K = p["shape"]
+        if w.dim() == 3:
+            raise RuntimeError(f"lt2_run: w has the reference's split-K layout [S, K/S, N] {tuple(w.shape)} "
+                               "(src/lt.cpp:58-59, wl=1); libojx reads the split-K chunks of W [N, K] in place, so "
+                               "pass W itself (FastProjections._split returns it)")
         if tuple(x.shape) != (M, K) or tuple(w.shape) != (N, K):
             raise RuntimeError("x / w do not match the plan's shape (w must be [N, K])")
         return ext.mm_splitk_f32(x, w, p["S"], tile=p["found"][idx])

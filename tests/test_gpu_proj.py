@@ -300,7 +300,7 @@ def _sk_tiles(pkg):
 def test_stream_k_family(pkg, ext, O, dev, M, N, K):
     """Persistent tiles: whole-tile waves, then the remainder's K iterations spread over the grid (S = pieces per
     tile). Every spread matches the oracle, repeats bit-exactly (the partials are summed in K order whatever the
-    arrival order), and leaves the workspace counters at zero for the next call."""
+    arrival order), whatever the workspace held before the call (it is scratch: filled with NaN bytes here)."""
     x, w = O.seeded_inputs(M, N, K, seed=M + N + K + 1)
     ref = O.linear_bf16(x, w)
     xd, wd = x.to(dev), w.to(dev)
@@ -308,19 +308,19 @@ def test_stream_k_family(pkg, ext, O, dev, M, N, K):
         base = None
         for S in (1, 2, 8, 16):
             _say(f"case stream-K M={M} N={N} K={K} tile={t} S={S}")
+            for buf, _ in ext._WS.values():
+                buf.fill_(0xFF)
             y = ext.mm(xd, wd, cfg=(t, S))
             _assert_tol(O, y, ref, f"tile {t} S {S}")
             assert torch.equal(y, ext.mm(xd, wd, cfg=(t, S))), f"tile {t} S {S} not deterministic"
             if S == 1:
                 base = y
-        for ws in ext._WS.values():
-            assert int(ws[:4096].count_nonzero()) == 0, "stream-K counters not returned to zero"
         assert base is not None
 
 
 def test_stream_k_epilogues_and_graph(pkg, ext, O, dev):
     """Fused SiLU.mul and residual epilogues through the persistent family with a stream-K remainder, eager and in
-    a replayed graph (the arrival counters must return to zero on every replay)."""
+    a replayed graph (every replay bit-equal to the eager result)."""
     M, I, K, N = 288, 1032, 640, 1024
     g = torch.Generator().manual_seed(21)
     x = torch.randn(M, K, generator=g).bfloat16()
