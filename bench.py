@@ -2,13 +2,13 @@
 
 Default run (the driver's contract): the BASELINE configs[1] workload — the fused gate-up projection with the
 SiLU.mul epilogue, x [288, 5120] bf16 ~ N(0,1), W_gu [2 x 17408, 5120] ~ N(0, 0.02^2), out [288, 17408] bf16 —
-as W untimed warm-up steps and then exactly K timed steps, captured in one HIP graph and replayed once between
-two synchronizations. A step is one call of the fused projection over the batch; the weights rotate over two
+as W untimed warm-up steps and then exactly K timed steps, captured in one HIP graph; the graph is replayed --reps
+times, each replay between two synchronizations, and the median replay gives the step time. A step is one call of the fused projection over the batch; the weights rotate over two
 copies (712 MB), more than the 256 MB Infinity Cache, so every step streams its weights from HBM.
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel (HIP events on the launch stream), the
 CPU baseline (the oracle's torch CPU path on a bounded sample of the same workload, on this host's cores) and the
-per-shape table at M = 7 / 288 / 539 for the five projection shapes.
+per-shape table at M = 7 / 64 / 288 / 539 / 2048 for the five projection shapes.
 
 Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
 the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV), --vs-hipblaslt
@@ -27,6 +27,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "bf16 proj GEMM TFLOP/s + HBM GB/s, % roofline, at M=7/288/539 on 1 MI355X"
+SHAPE_MS = (7, 64, 288, 539, 2048)   # the north star's M set for the per-shape table
 
 
 def load():
@@ -127,14 +128,19 @@ def main_default(args, pkg, ext, perf):
     torch.cuda.synchronize()
     graph.replay()  # upload / first replay (untimed)
     torch.cuda.synchronize()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # The K steps are timed REPS times (one replay of the K-step graph each, bracketed by synchronizations); the
+    # reported step time is the median replay divided by K. Every replay is reported in `replays_ms`.
     cur = torch.cuda.current_stream()
-    torch.cuda.synchronize()
-    a.record(cur)
-    graph.replay()
-    b.record(cur)
-    torch.cuda.synchronize()
-    ms = a.elapsed_time(b) / args.steps
+    reps = []
+    for _ in range(max(1, args.reps)):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        a.record(cur)
+        graph.replay()
+        b.record(cur)
+        torch.cuda.synchronize()
+        reps.append(a.elapsed_time(b))
+    ms = statistics.median(reps) / args.steps
     r = perf.roofline(M, N, K, "silu", ms * 1e-3)
     flops, nbytes = perf.work(M, N, K, "silu")
 
@@ -183,13 +189,13 @@ def main_default(args, pkg, ext, perf):
     shapes = {}
     if not args.no_shapes:
         for name in perf.SHAPES:
-            for m in (7, 288, 539):
+            for m in SHAPE_MS:
                 rr = measure_shape(ext, perf, name, m)
                 shapes[f"{name}_M{m}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}
     cpu = None if args.no_cpu else cpu_baseline(M, I, K)
     line = {
         "metric": METRIC, "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms, 5), "higher_is_better": True, "scaling": "weak",
+        "warmup": args.warmup, "ms_per_step": round(ms, 5), "replays_ms": [round(v, 4) for v in reps], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: seeded x ~ N(0,1), W ~ N(0,0.02^2), bf16; 2 rotating weight copies",
         "config": {"workload": "gate_up_silu: BASELINE configs[1], fused gate-up + SiLU.mul, M=288 K=5120 "
@@ -330,6 +336,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--reps", type=int, default=7, help="replays of the K-step graph; the median is reported")
     ap.add_argument("--sweep", action="store_true")
     ap.add_argument("--stack", action="store_true")
     ap.add_argument("--head", action="store_true")

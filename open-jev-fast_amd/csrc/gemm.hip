@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
       const int c = tid + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
       const bool ok = (W_CH % NT == 0 || c < W_CH) && k0 + col < ke;
-      rw[i] = bload(rsW, ok ? (uint32_t)(row * p.ldw + k0 + col) * 2u : kOOB);
+      rw[i] = bload_nt(rsW, ok ? (uint32_t)(row * p.ldw + k0 + col) * 2u : kOOB);
     }
 #pragma unroll
     for (int i = 0; i < CX; ++i) {
@@ -190,7 +190,7 @@ __global__ void __launch_bounds__(64 * NW) gemm_wd_kernel(const GemmParams p, co
     const bool kin = t * 32 < klim;
 #pragma unroll
     for (int f = 0; f < FN; ++f)
-      wr[slot][f] = __builtin_bit_cast(bf16x8, bload(rsW, kin ? woff[f] + (uint32_t)t * 64u : kOOB));
+      wr[slot][f] = __builtin_bit_cast(bf16x8, bload_nt(rsW, kin ? woff[f] + (uint32_t)t * 64u : kOOB));
   };
 
   uint4 rx[CX];
@@ -334,7 +334,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_w32_kernel(const GemmParams
 #pragma unroll
       for (int c = 0; c < G; ++c) {
         const bool ok = u * 64 + c * 8 < klim;
-        wr[slot][f][c] = bload_asm(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
+        wr[slot][f][c] = bload_asm_nt(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
       }
   };
   u32x4 rx[2][CX];
@@ -463,7 +463,8 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_w32_kernel(const GemmParams
         const f32x4 u = epi == EPI_SILU ? shfl4(v, 32) : v;
         const int n = n0 + (wn * FN + f) * 32 + 8 * rr + 4 * lh;
         const int m = m0 + (wm * FM + fm) * 32 + lr;
-        store4(p, epi, z, m, n, lh == 0, v, u);
+        if (epi == EPI_SILU) store_silu_pair(p, m, n, lh == 0, v, u);
+        else store4(p, epi, z, m, n, true, v, v);
       }
 #undef OJX_WAIT_W
 #undef OJX_WAIT_X
@@ -536,7 +537,7 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_w32d_kernel(const GemmParam
 #pragma unroll
       for (int c = 0; c < G; ++c) {
         const bool ok = u * 64 + c * 8 < klim;
-        wr[slot][f][c] = bload_asm(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
+        wr[slot][f][c] = bload_asm_nt(rsW, ok ? woff[f] + (uint32_t)(u * 128 + c * 16) : kOOB);
       }
   };
   auto xdma = [&](int buf, int st) {
@@ -631,7 +632,8 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_w32d_kernel(const GemmParam
         const f32x4 u = epi == EPI_SILU ? shfl4(v, 32) : v;
         const int n = n0 + (wn * FN + f) * 32 + 8 * rr + 4 * lh;
         const int m = m0 + (wm * FM + fm) * 32 + lr;
-        store4(p, epi, z, m, n, lh == 0, v, u);
+        if (epi == EPI_SILU) store_silu_pair(p, m, n, lh == 0, v, u);
+        else store4(p, epi, z, m, n, true, v, v);
       }
 #undef OJX_WAIT_W
 }
@@ -702,7 +704,8 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_dma_kernel(const GemmParams
       const bool isw = j < IW;
       const int ldsoff = isw ? j * 1024 : BN * 128 + (j - IW) * 1024;
       const bool ok = st * 64 + kcol[i] < ke - kb;
-      dma16(isw ? rsW : rsX, dst + ldsoff, ok ? voff[i] + (uint32_t)st * 128u : kOOB);
+      if (isw) dma16_nt(rsW, dst + ldsoff, ok ? voff[i] + (uint32_t)st * 128u : kOOB);
+      else dma16(rsX, dst + ldsoff, ok ? voff[i] + (uint32_t)st * 128u : kOOB);
     }
   };
 
@@ -797,6 +800,10 @@ struct TileEntry {
 #define OJX_SK(FN, FM, WN, WM)                                                                               \
   {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 2 * (WN * FN * 16 + WM * FM * 16) * 128, 5},    \
    gemm_sk_kernel<FN, FM, WN, WM>, gemm_sk_fixup_kernel<FN, FM, WN, WM>}
+// K-interleaved pair tiles: BN = 16 FW W rows, BM = 16 (4 FX + XE) x rows, 8 waves, 64-k stages, two LDS buffers
+#define OJX_KX(FW, FX, XE)                                                                                   \
+  {{16 * FW, 16 * (4 * FX + XE), 64, 4, 2, 512, (3 * 16 * FW + 2 * 16 * (4 * FX + XE)) * 128, 6},           \
+   gemm_kx_kernel<FW, FX, XE>}
 #define OJX_W32(FN, FM, WN, WM, DG)                                                                          \
   {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 72 * 2, 3},                   \
    gemm_w32_kernel<FN, FM, WN, WM, DG>}
@@ -886,6 +893,10 @@ static const TileEntry kTiles[] = {
     OJX_SK(4, 3, 4, 2),             // 77 256 x 96
     OJX_SK(2, 9, 4, 2),             // 78 128 x 288
     OJX_SK(3, 9, 4, 2),             // 79 192 x 288: 182 W tiles at M <= 288, one round on 256 CUs
+    OJX_KX(9, 4, 2),                // 80 144 x 288 K-interleaved pairs: 242 W tiles of the gate-up at M <= 288
+    OJX_KX(8, 4, 2),                // 81 128 x 288
+    OJX_KX(9, 2, 1),                // 82 144 x 144
+    OJX_KX(8, 4, 0),                // 83 128 x 256
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

@@ -17,6 +17,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, in
 __device__ __forceinline__ uint4 bload(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
 }
+// Non-temporal load (cache-policy bit nt): for the weight stream, read once per call, so that it does not evict the
+// activations every workgroup shares from L2. Measured on MI355X: a weight stream with the hint reaches 6.4 TB/s
+// against 6.1 without, and streams that mix weights and L2-resident activations run about 9% faster.
+__device__ __forceinline__ uint4 bload_nt(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+}
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor's range: the load returns zeros
 
 // The same descriptor as four dwords, for loads issued from inline assembly. The compiler's wait-count pass does
@@ -39,6 +45,11 @@ __device__ __forceinline__ u32x4 bload_asm(const u32x4& r, uint32_t off) {
   asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(r) : "memory");
   return v;
 }
+__device__ __forceinline__ u32x4 bload_asm_nt(const u32x4& r, uint32_t off) {  // with the non-temporal hint
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(v) : "v"(off), "s"(r) : "memory");
+  return v;
+}
 // Same load into accumulation registers (AGPRs): used for data that only goes on to LDS, so the compiler never has
 // a reason to copy or spill it before the explicit wait (it cannot tell that the load is still in flight).
 __device__ __forceinline__ u32x4 bload_asm_agpr(const u32x4& r, uint32_t off) {
@@ -56,6 +67,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 // inline there, the address-space cast stops the host pass from emitting the kernels' launch stubs.)
 __device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 0);
+}
+
+// The same DMA with the non-temporal hint: the lines are not kept in L2 for reuse. For operands that are read once
+// per call (the weight stream), so that they do not evict operands that other workgroups are about to read.
+__device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 2);
 }
 
 // Workgroup barrier that orders LDS only. __syncthreads() is a full workgroup fence, which on gfx9 waits for every
@@ -103,11 +120,31 @@ __device__ __forceinline__ f32x4 shfl4(const f32x4 v, int mask) {
   return f32x4{__shfl_xor(v[0], mask), __shfl_xor(v[1], mask), __shfl_xor(v[2], mask), __shfl_xor(v[3], mask)};
 }
 
+// Fused SiLU.mul of one fragment with the work split over both lanes of each gate/up pair: after the exchange the
+// gate lane (even lane group, gate columns n .. n+3) and its partner (up columns of the same outputs) each hold all
+// eight values, and each computes two of the four outputs, so no lane idles through the exp and the division.
+// Output column of lane: (gate column) / 2, + 2 for the partner.
+__device__ __forceinline__ void store_silu_pair(const GemmParams& p, const int m, const int n, const bool gate,
+                                                const f32x4 v, const f32x4 u) {
+  const int ng = gate ? n : n - 4;  // the pair's gate column
+  if (m >= p.M || ng >= p.N) return;
+  const float g0 = gate ? v[0] : u[2], g1 = gate ? v[1] : u[3];
+  const float u0 = gate ? u[0] : v[2], u1 = gate ? u[1] : v[3];
+  const uint32_t o0 = f2bf(rbf(silu_f(rbf(g0))) * rbf(u0));
+  const uint32_t o1 = f2bf(rbf(silu_f(rbf(g1))) * rbf(u1));
+  uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (ng >> 1) + (gate ? 0 : 2);
+  *reinterpret_cast<uint32_t*>(dst) = o0 | (o1 << 16);
+}
+
 // Epilogue of one 16x16 accumulator fragment: lane holds v[e] = y[m][n + e]; lane group lg = lane / 16.
 __device__ __forceinline__ void store_tile(const GemmParams& p, const int epi, const int z, const int m, const int n,
                                            const int lg, const f32x4 v) {
-  const f32x4 u = epi == EPI_SILU ? shfl4(v, 16) : v;  // all lanes take part in the exchange
-  store4(p, epi, z, m, n, (lg & 1) == 0, v, u);
+  if (epi == EPI_SILU) {
+    const f32x4 u = shfl4(v, 16);  // all lanes take part in the exchange
+    store_silu_pair(p, m, n, (lg & 1) == 0, v, u);
+    return;
+  }
+  store4(p, epi, z, m, n, true, v, v);
 }
 
 
@@ -119,4 +156,7 @@ template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_kernel(const GemmParams p, const int epi);
 template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_fixup_kernel(const GemmParams p, const int epi);
+// K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
+template <int FW, int FX, int XE>
+__global__ void gemm_kx_kernel(const GemmParams p, const int epi);
 }  // namespace ojx

@@ -1,0 +1,296 @@
+// bf16 projection GEMM for gfx950 with K-interleaved wave pairs: y[M,N] = x[M,K] . W[N,K]^T, fp32 accumulation on
+// v_mfma_f32_16x16x32_bf16, epilogues fused into the store (same modes as gemm.hip).
+//
+// Replaces the reference's cuBLASLt GEMM (src/lt.cpp:43-55, through _mm, src/fastmodel.py:168-175) at the M where
+// a projection needs whole-M tiles: the tile covers all of x (M <= BM), so each W row is read from HBM once, and
+// BN is chosen so that the tile count fills the 256 CUs (144 W rows for the 34816-row gate-up: 242 tiles).
+//
+// Why this shape of kernel:
+//   * The 16x16 fragments of a BN x BM tile do not split evenly over 8 waves for the tile sizes that fill the chip
+//     (9 x 18 fragments for 144 x 288). Instead the tile is split over the four SIMDs (group g = wave & 3): group g
+//     owns W fragments 0..FW-1 times x fragments g*FX .. g*FX+FX-1, plus an equal share of the XE x fragments left
+//     over (x fragment 4*FX + ..., EW of its W fragments). The two waves of a group (wave g and wave g+4) own the
+//     same fragments and interleave K: within every 64-k stage, wave g multiplies the first 32 k and wave g+4 the
+//     second. Every wave therefore carries FW*FX + EW accumulators (41 for 144 x 288, 164 registers) and reads
+//     FW + FX + 1 fragments per k32 step: 14 LDS fragment reads per 41 MFMAs, against 24 per 54 for eight 48 x 144
+//     wave tiles, with two waves per SIMD to hide LDS latency and barriers.
+//   * The pair's partial sums are added through LDS at the end of the tile (two exchanges of half the fragments),
+//     so each wave then stores half of its group's outputs. The sum over k is (even 32-k blocks) + (odd 32-k
+//     blocks): deterministic, but a different rounding order from the other tile families.
+//   * Operands reach LDS by DMA (buffer_load ... lds, 16 B per lane, one 8-row x 128 B block per wave instruction)
+//     in stages of 64 k, two buffers: stage t+1 is in flight while stage t is multiplied. LDS rows are 128 B with
+//     the 16-byte chunks XOR-swizzled by (row / 2) mod 8, so the 16 rows one ds_read_b128 touches hit distinct banks.
+//     Half of a stage's DMA instructions go out right after the barrier that frees their buffer, the rest one per
+//     MFMA group of the following groups.
+//   * A wave walks its W fragments starting at its first extra fragment (rotated order), so the extra MFMAs sit
+//     in the first EW groups of every stage for every wave: straight-line code for all groups.
+#include "gemm_common.h"
+
+namespace ojx {
+
+namespace {
+
+__device__ __forceinline__ void kx_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+template <int FW, int FX, int XE>
+struct KxShape {
+  static constexpr int BN = 16 * FW, BM = 16 * (4 * FX + XE);
+  static constexpr int RB = 128, WD = 3;                          // W ring depth (stages of 64 k)
+  static constexpr int LDS = (WD * BN + 2 * BM) * RB;             // W ring + x double buffer
+  static constexpr int NW = 8, NBLK = (BN + BM) / 8, GPW = (NBLK + NW - 1) / NW;
+  static constexpr int EW = XE == 0 ? 0 : XE == 1 ? (FW + 3) / 4 : (FW + 1) / 2;  // extra W fragments per group
+  static constexpr int NX = FX + (XE > 0 ? 1 : 0);                                  // x fragments per wave
+  static constexpr int NACC = FW * FX + EW;                                         // accumulators per wave
+  static constexpr int HF = (NACC + 1) / 2;                                         // fragments reduced by wave g
+  static_assert(XE >= 0 && XE <= 2, "0..2 leftover x fragments");
+  static_assert(4 * HF * 64 * 16 <= LDS, "the pair exchange must fit the stage buffers");
+  static_assert(LDS <= 160 * 1024, "LDS");
+};
+
+// REV (two leftover x fragments only): the group walks its W fragments from the last one down, so that its extra
+// fragments (the upper half) come first; the other groups walk upwards. Either way the walk is static code.
+template <int FW, int FX, int XE, int EPI, bool REV>
+__device__ __forceinline__ void kx_body(const GemmParams& p) {
+  using S = KxShape<FW, FX, XE>;
+  constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW, GPW = S::GPW;
+  constexpr int EW = S::EW, NX = S::NX, NACC = S::NACC, HF = S::HF;
+  constexpr int BK = 64;
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // W ring, then x double buffer
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = wave & 3, h = wave >> 2;
+  const int lr = lane & 15, lg = lane >> 4;
+
+  // XCD-aware logical tile id (workgroup b runs on XCD b mod 8); M tile fastest, then split, then N tile.
+  const int G = gridDim.x, b = blockIdx.x;
+  const int q = G >> 3, r = G & 7, xcd = b & 7;
+  const int L = xcd * q + min(xcd, r) + (b >> 3);
+  const int tm = L % p.tiles_m;
+  const int t2 = L / p.tiles_m;
+  const int z = t2 % p.splits;
+  const int tn = t2 / p.splits;
+  const int n0 = tn * BN, m0 = tm * BM;
+  const int kb = z * p.kchunk;
+  const int ke = min(p.K, kb + p.kchunk);
+  const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
+
+  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+
+  // ------------------------------------------------------------------ fragment ownership
+  // extra fragments: x fragment xe, W fragments wstart .. wstart + EW - 1 (walked first)
+  const int xe = 4 * FX + (XE == 2 ? (g >> 1) : 0);
+  const int wnom = XE == 1 ? g * EW : XE == 2 ? (g & 1) * EW : 0;  // first extra this group stores
+  const int wstart = XE == 2 ? (REV ? FW - EW : 0) : min(wnom, FW - EW);
+  // W fragment at walk position pp
+  auto wfrag = [&](int pp) -> int {
+    if constexpr (XE == 2) return REV ? FW - 1 - pp : pp;
+    const int j = wstart + pp;
+    return j >= FW ? j - FW : j;
+  };
+  // LDS byte offsets (within a stage) of this lane's reads for its k half: row r0 + lr, chunk 4h + lg swizzled
+  const uint32_t ro = (uint32_t)(lr * RB + (((4 * h + lg) ^ (lr >> 1)) & 7) * 16);
+  uint32_t woff[FW];
+#pragma unroll
+  for (int pp = 0; pp < FW; ++pp) woff[pp] = (uint32_t)(wfrag(pp) * 16 * RB) + ro;
+  uint32_t xoff[NX];
+#pragma unroll
+  for (int i = 0; i < FX; ++i) xoff[i] = (uint32_t)((g * FX + i) * 16 * RB) + ro;
+  if constexpr (XE > 0) xoff[FX] = (uint32_t)(xe * 16 * RB) + ro;
+
+  // ------------------------------------------------------------------ LDS rings and DMA pattern
+  // LDS: a ring of WD = 3 stages of W (BN rows x 128 B = 64 k) and a ring of 2 stages of x (BM rows), 16-byte chunks
+  // XOR-swizzled by (row / 2) mod 8 within each region. A wave reads its x fragments of a stage into registers right
+  // after the barrier that publishes the stage and keeps them for the whole stage, so a second barrier a few MFMA
+  // groups later frees that x buffer: the DMAs issued then (batch t, issued as stage t begins) fetch x and W of
+  // stage t+2. Both operands get two stages to arrive; the weights come from HBM, x (the same rows for every
+  // workgroup) mostly from L2, and a wave's DMAs complete in issue order, so the x and W traffic share one queue.
+  constexpr int WST = BN * RB, XST = BM * RB;
+  uint8_t* const wring = smem;
+  uint8_t* const xring = smem + S::WD * WST;
+  constexpr int XB = BM / 8, WB = BN / 8, NB = XB + WB;
+  // Batch block c = wave + 8 i (i < GPW): x block c if c < XB, else W block c - XB; waves past the end repeat the
+  // last block (same bytes to the same place), so every wave issues GPW DMAs per batch. Per-lane parts of the
+  // offsets for an even and an odd block (the swizzle depends on the block's parity); the block's own part is
+  // wave-uniform and computed at issue.
+  int kcp[2];
+  uint32_t lx[2], lw[2];
+#pragma unroll
+  for (int par = 0; par < 2; ++par) {
+    kcp[par] = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;
+    lx[par] = (uint32_t)(((lane >> 3) * p.ldx + kcp[par]) * 2);
+    lw[par] = (uint32_t)(((lane >> 3) * p.ldw + kcp[par]) * 2);
+  }
+  // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
+  auto dma = [&](int st, int lo, int hi) {
+    const int k0 = kb + st * BK;
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) {
+      if (i < lo || i >= hi) continue;
+      const int c = min(wave + i * NW, NB - 1);  // wave-uniform
+      const bool isw = c >= XB;
+      const int blk = isw ? c - XB : c, par = blk & 1;
+      const bool ok = st < nk && k0 + kcp[par] < ke;
+      if (isw) {
+        const uint32_t o = (uint32_t)(blk * 8 * p.ldw * 2) + lw[par] + (uint32_t)k0 * 2u;
+        dma16_nt(rsW, wring + (st % S::WD) * WST + blk * 1024, ok ? o : kOOB);
+      } else {
+        const uint32_t o = (uint32_t)(blk * 8 * p.ldx * 2) + lx[par] + (uint32_t)k0 * 2u;
+        dma16(rsX, xring + (st & 1) * XST + blk * 1024, ok ? o : kOOB);
+      }
+    }
+  };
+
+  f32x4 acc[FW][FX], acce[EW > 0 ? EW : 1];
+#pragma unroll
+  for (int i = 0; i < FW; ++i)
+#pragma unroll
+    for (int j = 0; j < FX; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < (EW > 0 ? EW : 1); ++i) acce[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+#define OJX_KX_RD(sb, off) (*reinterpret_cast<const bf16x8*>((sb) + (off)))
+  // groups: one per W fragment (position pp), FX MFMAs (+1 for the first EW); the last PD groups of a stage run
+  // after the barrier that publishes the next stage, with their operands already in registers
+  constexpr int PD = 2;
+  constexpr int NMG = FW - PD;
+  constexpr int H0 = (GPW + 1) / 2;           // DMAs right after the barrier
+  constexpr int NDG = GPW - H0 < NMG - 2 ? GPW - H0 : (NMG - 2 > 0 ? NMG - 2 : 0);  // groups carrying one more
+  constexpr int H1 = GPW - NDG;               // issued after the barrier (H0 plus what does not fit the groups)
+
+  bf16x8 xc[NX], wr[PD + 1];
+  if (nk > 0) {
+    dma(0, 0, GPW);
+    dma(1, 0, GPW);
+    wait_vmcnt<GPW>();  // stage 0 has landed
+    kx_barrier();
+#pragma unroll
+    for (int i = 0; i < NX; ++i) xc[i] = OJX_KX_RD(xring, xoff[i]);
+#pragma unroll
+    for (int d = 0; d < PD; ++d) wr[d] = OJX_KX_RD(wring, woff[d]);
+    kx_barrier();       // every wave holds its x fragments of stage 0: x slot 0 is free
+    dma(2, 0, H1);
+  }
+  for (int t = 0; t < nk; ++t) {
+    const uint8_t* sw = wring + (t % S::WD) * WST;
+#pragma unroll
+    for (int pp = 0; pp < NMG; ++pp) {
+      wr[(pp + PD) % (PD + 1)] = OJX_KX_RD(sw, woff[pp + PD]);
+      const bf16x8 a = wr[pp % (PD + 1)];
+#pragma unroll
+      for (int i = 0; i < FX; ++i) acc[pp][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[i], acc[pp][i], 0, 0, 0);
+      if constexpr (EW > 0)
+        if (pp < EW) acce[pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[FX], acce[pp], 0, 0, 0);
+      if (pp < NDG) dma(t + 2, H1 + pp, H1 + pp + 1);
+    }
+    bf16x8 xn[NX], wn[PD];
+    const bool more = t + 1 < nk;
+    if (more) {
+      wait_vmcnt<GPW>();  // stage t+1 has landed (only the batch of stage t+2 may be outstanding)
+      kx_barrier();       // every wave's has, and every wave's W reads of stage t are done
+      const uint8_t* nw = wring + ((t + 1) % S::WD) * WST;
+      const uint8_t* nx = xring + ((t + 1) & 1) * XST;
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xn[i] = OJX_KX_RD(nx, xoff[i]);
+#pragma unroll
+      for (int d = 0; d < PD; ++d) wn[d] = OJX_KX_RD(nw, woff[d]);
+    }
+#pragma unroll
+    for (int pp = NMG; pp < FW; ++pp) {
+      const bf16x8 a = wr[pp % (PD + 1)];
+#pragma unroll
+      for (int i = 0; i < FX; ++i) acc[pp][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[i], acc[pp][i], 0, 0, 0);
+      if constexpr (EW > 0)
+        if (pp < EW) acce[pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[FX], acce[pp], 0, 0, 0);
+    }
+    if (more) {
+      kx_barrier();       // every wave holds its x fragments of stage t+1: that x slot takes stage t+3
+      dma(t + 3, 0, H1);
+#pragma unroll
+      for (int i = 0; i < NX; ++i) xc[i] = xn[i];
+#pragma unroll
+      for (int d = 0; d < PD; ++d) wr[d] = wn[d];
+    }
+  }
+#undef OJX_KX_RD
+  wait_vmcnt<0>();
+  kx_barrier();  // LDS is free for the pair exchange
+
+  // ------------------------------------------------------------------ pair reduction
+  // Fragment f of a wave: acc[f / FX][f % FX] for f < FW FX, then acce[f - FW FX]. Wave g (h = 0) finishes
+  // fragments 0 .. HF-1 and wave g+4 (h = 1) the rest. Two rounds through LDS (both halves at once would not fit):
+  // wave g+4 hands over its first half, then wave g its second.
+  float* const xch = reinterpret_cast<float*>(smem);
+#pragma unroll
+  for (int round = 0; round < 2; ++round) {
+    const int lo = round == 0 ? 0 : HF, hi = round == 0 ? HF : NACC;
+    if (h != round) {  // the writer of this round
+#pragma unroll
+      for (int f = lo; f < hi; ++f) {
+        const f32x4 v = f < FW * FX ? acc[f / FX][f % FX] : acce[f - FW * FX];
+        *reinterpret_cast<f32x4*>(xch + ((g * HF + f - lo) * 64 + lane) * 4) = v;
+      }
+    }
+    kx_barrier();
+    if (h == round) {
+#pragma unroll
+      for (int f = lo; f < hi; ++f) {
+        const f32x4 o = *reinterpret_cast<const f32x4*>(xch + ((g * HF + f - lo) * 64 + lane) * 4);
+        if (f < FW * FX) acc[f / FX][f % FX] += o;
+        else acce[f - FW * FX] += o;
+      }
+    }
+    if (round == 0) kx_barrier();  // round 1 writes over the same LDS
+  }
+
+  // ------------------------------------------------------------------ epilogue
+  // lane holds v[e] = y[m][n + e]: m = m0 + 16 xf + lr, n = n0 + 16 wf + 4 lg
+#pragma unroll
+  for (int f = 0; f < NACC; ++f) {
+    if ((f < HF) != (h == 0)) continue;
+    int wf, xf;
+    bool keep = true;
+    if (f < FW * FX) {
+      wf = wfrag(f / FX);
+      xf = g * FX + f % FX;
+    } else {
+      wf = wfrag(f - FW * FX);
+      xf = xe;
+      keep = wf >= wnom;  // extras that overlap the neighbouring group's are stored by that group
+    }
+    const f32x4 v = f < FW * FX ? acc[f / FX][f % FX] : acce[f - FW * FX];
+    if (EPI == EPI_SILU) {
+      const f32x4 u = shfl4(v, 16);  // every lane takes part in the exchange
+      if (keep) store_silu_pair(p, m0 + xf * 16 + lr, n0 + wf * 16 + lg * 4, (lg & 1) == 0, v, u);
+    } else if (keep) {
+      store4(p, EPI, z, m0 + xf * 16 + lr, n0 + wf * 16 + lg * 4, true, v, v);
+    }
+  }
+}
+
+}  // namespace
+
+template <int FW, int FX, int XE, int EPI>
+__device__ __forceinline__ void kx_dir(const GemmParams& p) {
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true>(p);
+  else kx_body<FW, FX, XE, EPI, false>(p);
+}
+
+template <int FW, int FX, int XE>
+__global__ void __launch_bounds__(512) gemm_kx_kernel(const GemmParams p, const int epi) {
+  if (epi == EPI_SILU) kx_dir<FW, FX, XE, EPI_SILU>(p);
+  else if (epi == EPI_RESID) kx_dir<FW, FX, XE, EPI_RESID>(p);
+  else if (epi == EPI_F32) kx_dir<FW, FX, XE, EPI_F32>(p);
+  else kx_dir<FW, FX, XE, EPI_BF16>(p);
+}
+
+// Tile shapes of this family (registered in gemm.hip's tile table): BN x BM = 16 FW x 16 (4 FX + XE).
+template __global__ void gemm_kx_kernel<9, 4, 2>(const GemmParams, const int);  // 144 x 288
+template __global__ void gemm_kx_kernel<8, 4, 2>(const GemmParams, const int);  // 128 x 288
+template __global__ void gemm_kx_kernel<9, 2, 1>(const GemmParams, const int);  // 144 x 144
+template __global__ void gemm_kx_kernel<8, 4, 0>(const GemmParams, const int);  // 128 x 256
+
+}  // namespace ojx

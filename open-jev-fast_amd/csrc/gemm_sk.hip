@@ -174,7 +174,8 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       const uint32_t o_ = i < GW ? dW0 + i * stepW : real_ ? dX0 + (i - GW) * stepX : dXl;                 \
       const bool ok_ = (k0) + (real_ ? kcol : kcoll) < ke;                                                 \
       const int blk_ = real_ ? wave + i * NW : NBLK - 1;                                                   \
-      dma16(i < GW ? rsW : rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);              \
+      if (i < GW) dma16_nt(rsW, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);               \
+      else dma16(rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);                         \
     }                                                                                                      \
   } while (0)
     // Fragment reads. The stationary operand is held for a whole k32 step (both steps' fragments in registers);

@@ -249,7 +249,8 @@ def test_fastprojections_reference_call_pattern(pkg, ext, O, dev, monkeypatch):
     assert torch.equal(h1, e1[0]) and torch.equal(hn1, e1[1]), "_res did not run the plan's configuration"
     m = P._silu_mul(P._mm(hn1, d.w_gu))
     m_fused = P._mm_silu(hn1, d.w_gu_packed)
-    assert torch.equal(m, m_fused), "GEMM -> silu_mul_lut and the fused gate-up differ"
+    # the two paths may run tile families with different K summation orders: equal to rounding, both vs the oracle
+    _assert_tol(O, m_fused, m, "fused gate-up vs GEMM -> silu_mul_lut")
     h2, hn2 = P._res(h1, m, d.w_down_sk, d.sk_down, w1, mask, w=d.w_down)
     e2 = ext.mm_residual_rmsnorm(h1, m, w_down, w1, mask, 1e-6)
     assert torch.equal(h2, e2[0]) and torch.equal(hn2, e2[1])
@@ -262,6 +263,7 @@ def test_fastprojections_reference_call_pattern(pkg, ext, O, dev, monkeypatch):
     _assert_tol(O, c(hn1), rhn1, "_res out hn")
     rm = O.gate_up_silu(c(hn1), w_gate.cpu(), w_up.cpu())
     _assert_tol(O, c(m), rm, "_silu_mul(_mm)")
+    _assert_tol(O, c(m_fused), rm, "_mm_silu")
     rh2, rhn2 = O.residual_proj(c(h1), c(m), w_down.cpu(), w1.cpu(), c(mask), 1e-6, S=2)
     _assert_tol(O, c(h2), rh2, "_res down h")
     _assert_tol(O, c(hn2), rhn2, "_res down hn")

@@ -55,19 +55,22 @@ def test_mm_planned_and_f64(pkg, ext, O, dev, M, N, K):
 
 def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
     """Without split-K the tiles of one MFMA shape sum K in the same order: outputs are bit-identical across those
-    tiles and across runs (16x16x32 families 0-2; the 32x32x16 families 3-4 among themselves)."""
+    tiles and across runs (16x16x32 families 0-2 and 5; the 32x32x16 families 3-4 among themselves; the
+    K-interleaved family 6, which adds the sums of the even and odd 32-k blocks, among itself)."""
     M, N, K = 96, 512, 1024
     x, w = O.seeded_inputs(M, N, K, seed=3)
     xd, wd = x.to(dev), w.to(dev)
     _say("case tile invariance")
     base = {}
     for t in _tiles(pkg):
-        shape = 32 if pkg._lib.tile_info(t)["family"] in (3, 4) else 16
+        fam = pkg._lib.tile_info(t)["family"]
+        shape = 32 if fam in (3, 4) else "kx" if fam == 6 else 16
         y = ext.mm(xd, wd, cfg=(t, 1))
         if shape not in base:
             base[shape] = y
         assert torch.equal(y, base[shape]), f"tile {t}"
-    assert len(base) == 2
+        assert torch.equal(y, ext.mm(xd, wd, cfg=(t, 1))), f"tile {t} not deterministic"
+    assert len(base) == 3
     for S in (2, 4):
         a = ext.mm(xd, wd, cfg=(6, S))
         assert torch.equal(a, ext.mm(xd, wd, cfg=(6, S))), "split-K not deterministic"
@@ -170,6 +173,10 @@ def test_gate_up_merge_and_fusion_bitexact(pkg, ext, O, dev):
     assert torch.equal(gu[:, I:], ext.mm(x, wu, cfg=(6, 1)))
     fused = ext.mm_silu_mul(x, ext.pack_gate_up(wg, wu), cfg=(6, 1))
     assert torch.equal(fused, ext.silu_mul(gu))
+    kx = [t for t in _tiles(pkg) if pkg._lib.tile_info(t)["family"] == 6]
+    for t in kx:  # the K-interleaved family has its own K order: fused == GEMM -> silu_mul with the same tile
+        gu_t = ext.mm(x, torch.cat([wg, wu], 0).contiguous(), cfg=(t, 1))
+        assert torch.equal(ext.mm_silu_mul(x, ext.pack_gate_up(wg, wu), cfg=(t, 1)), ext.silu_mul(gu_t)), f"tile {t}"
     tab, _ = ext.act_tables(x)
     assert torch.equal(ext.silu_mul_lut(gu, tab), ext.silu_mul(gu))
 
