@@ -116,6 +116,22 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
                               int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
                               ojx_stream_t stream);
 
+/* Bytes of the static device scratch behind ojx_gemm_residual_rmsnorm_noalloc (one array per GPU). */
+#define OJX_NOALLOC_SCRATCH_BYTES (32LL << 20)
+
+/* ojx_gemm_residual_rmsnorm without a workspace argument and without any allocation: no hipMalloc / hipFree and no
+ * allocating library call, on any call. No counterpart in the reference: it is for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid allocation). The kernels' scratch (split-K
+ * planes, stream-K partial tiles) lives in a file-scope device array of OJX_NOALLOC_SCRATCH_BYTES per GPU, which
+ * each GPU the library runs on holds until the process ends. With cfg == NULL the plan's configuration is used with
+ * its split-K count (or stream-K spread) lowered until its workspace fits the scratch; an explicit cfg whose
+ * workspace exceeds the scratch is rejected with OJX_ERR_WORKSPACE. Every call on one GPU shares that GPU's array:
+ * calls that overlap on one GPU (different streams, or concurrent host threads) race and must be serialized by the
+ * caller. Results are bit-identical to ojx_gemm_residual_rmsnorm with the same configuration. */
+int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* residual, const float* w1,
+                                      const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M,
+                                      int64_t N, int64_t K, const ojx_cfg* cfg, ojx_stream_t stream);
+
 /* Scoring head: scores[r] = sum_j float(hn[lastidx[r]][j]) * w[j] + bias[0] (bias may be NULL), fp32.
  * hn bf16 [rows, H] contiguous, lastidx int64 [R], w fp32 [H], scores fp32 [R]. Replaces the last matmul of the
  * forward, mdl.head(hn[lastidx].float()).squeeze(-1) (src/server.py:37,57,129; hn[lastidx] is

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <mutex>
 #include <string>
 
 namespace {
@@ -247,6 +248,32 @@ int check_rows(int64_t M, int64_t H) {
     if (rc_ != OJX_OK) return rc_;  \
   } while (0)
 
+// ------------------------------------------------------------------------------------- static scratch
+// Device memory of ojx_gemm_residual_rmsnorm_noalloc: one array per GPU, held for the life of the process. In host
+// code `scratch` is only a handle for the symbol lookup; kernels get the device address from hipGetSymbolAddress.
+constexpr int64_t kScratchBytes = OJX_NOALLOC_SCRATCH_BYTES;
+__device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices];
+
+// The scratch array's address on the current device (looked up once per device, with that device current).
+int scratch_ptr(void** out) {
+  int dev = 0;
+  OJX_TRY(hip_check(hipGetDevice(&dev), "hipGetDevice"));
+  if (dev < 0 || dev >= kMaxDevices) return fail(OJX_ERR_ARG, "device %d out of range [0, %d)", dev, kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    OJX_TRY(hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"));
+    if (p == nullptr) return fail(OJX_ERR_HIP, "hipGetSymbolAddress(scratch) gave a null address");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return OJX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -259,7 +286,11 @@ const char* ojx_last_error(void) { return g_err.c_str(); }
 // caller can tell whether the loaded binary matches a source tree.
 const char* ojx_version(void) { return "ojx 0.2 gfx950 src:" OJX_SRC_DIGEST; }
 
-int ojx_init(void) { return hip_check(ojx::init_tiles(), "kernel attribute setup"); }
+int ojx_init(void) {
+  OJX_TRY(hip_check(ojx::init_tiles(), "kernel attribute setup"));
+  void* p = nullptr;
+  return scratch_ptr(&p);
+}
 
 int ojx_num_tiles(void) { return ojx::num_tiles(); }
 
@@ -442,6 +473,33 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st));
   return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(residual), nullptr, parts, c.splitk, M * N,
                                            w1, rowmask, eps, h, hn, (int)M, (int)N, st), "rmsnorm launch");
+}
+
+int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* residual, const float* w1,
+                                      const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M,
+                                      int64_t N, int64_t K, const ojx_cfg* cfg, ojx_stream_t stream) {
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;
+  ojx_cfg c{};
+  OJX_TRY(resolve(M, N, K, OJX_KIND_RESIDUAL, cfg, &c));
+  int64_t need = workspace_for(c, M, N, K);
+  if (cfg != nullptr && need > kScratchBytes)
+    return fail(OJX_ERR_WORKSPACE, "config (tile %d, splitk %d) needs %lld bytes of workspace; the static scratch of "
+                "the allocation-free entry point holds %lld", c.tile, c.splitk, (long long)need,
+                (long long)kScratchBytes);
+  // The plan's own configuration, with its split-K count (or stream-K spread) lowered until its workspace fits.
+  while (need > kScratchBytes && c.splitk > 1) {
+    --c.splitk;
+    if (!cfg_fits(M, N, K, c)) continue;
+    need = workspace_for(c, M, N, K);
+  }
+  if (need > kScratchBytes)
+    return fail(OJX_ERR_WORKSPACE, "M=%lld N=%lld K=%lld needs %lld bytes of workspace, more than the static scratch "
+                "(%lld)", (long long)M, (long long)N, (long long)K, (long long)need, (long long)kScratchBytes);
+  void* ws = nullptr;
+  OJX_TRY(scratch_ptr(&ws));
+  return ojx_gemm_residual_rmsnorm(x, w, residual, w1, rowmask, eps, h_out, hn_out, M, N, K, ws, kScratchBytes, &c,
+                                   stream);
 }
 
 int ojx_add_rmsnorm(const void* x, const void* delta, const float* w1, const int32_t* rowmask, float eps,
