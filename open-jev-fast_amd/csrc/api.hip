@@ -177,9 +177,12 @@ int check_dims(int64_t M, int64_t N, int64_t K) {
 }
 
 // One GEMM launch with the given tile / split count and epilogue.
+// With hn_out (persistent family, residual epilogue, split tiles only): the split-tile pass is fused with the
+// RMSNorm of the rows, writing h and hn.
 int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
          const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st, void* ws = nullptr,
-         int64_t ws_off = 0) {
+         int64_t ws_off = 0, const float* w1 = nullptr, const int32_t* rowmask = nullptr, float eps = 0.f,
+         uint16_t* hn_out = nullptr) {
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
   ojx::GemmParams p;
   p.W = static_cast<const uint16_t*>(w);
@@ -214,6 +217,9 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
     }
   }
   if ((int64_t)p.tiles_n * p.tiles_m * p.splits >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "grid too large");
+  if (hn_out != nullptr)
+    return hip_check(ojx::launch_gemm_residual_rmsnorm_sk(c.tile, p, w1, rowmask, eps, hn_out, st, grid),
+                     "gemm + row pass launch");
   return hip_check(ojx::launch_gemm(c.tile, epi, p, st, grid), "gemm launch");
 }
 
@@ -462,6 +468,12 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   uint16_t* hn = static_cast<uint16_t*>(hn_out);
   if (c.splitk == 1 || is_sk(c.tile)) {
     OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
+    if (hn != nullptr && is_sk(c.tile) && sk_plan(ojx::tile_info(c.tile), M, N, K, c.splitk).partial) {
+      // persistent plan with split tiles: GEMM, then one launch that sums the pieces, adds the residual and
+      // normalises each row
+      return gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, w1, rowmask,
+                  eps, hn);
+    }
     OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0));
     if (hn == nullptr) return OJX_OK;
     return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,

@@ -17,7 +17,6 @@
 
 namespace ojx {
 
-__device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
 
 // a[v] = sum over the S planes of the float4 at src + 4 v, added in ascending plane order. The loads go out eight
 // planes at a time (indices clamped, extra planes not added) so that S planes cost about S/8 memory latencies
@@ -77,18 +76,6 @@ __global__ void __launch_bounds__(256) reduce_silu_k(const float* __restrict__ p
   *reinterpret_cast<uint2*>(out + (int64_t)m * ldo + blk * 4) = make_uint2(pack2(o0, o1), pack2(o2, o3));
 }
 
-// Sum over the whole workgroup (wave64 butterfly, then one value per wave through LDS).
-__device__ __forceinline__ float block_sum(float v, float* red) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
-  if (lane == 0) red[wid] = v;
-  __syncthreads();
-  float t = 0.f;
-  for (int i = 0; i < nw; ++i) t += red[i];
-  return t;
-}
-
 // One workgroup per row, H/8 threads, 8 contiguous elements per thread.
 // MODE 0: h = x (no add); 1: h = bf16(x + delta); 2: h = bf16(x + bf16(sum of the S fp32 planes)). HN: write hn.
 // Both are template parameters so that each variant is straight-line code and its loads (planes, x, w1) go out
@@ -132,20 +119,7 @@ __global__ void __launch_bounds__(1024) add_rmsnorm_k(const uint16_t* __restrict
     *reinterpret_cast<uint4*>(h_out + row * H + i) =
         make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
   }
-  if constexpr (HN) {
-    const bool keep = rowmask == nullptr || rowmask[row] != 0;
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
-    ss = block_sum(ss, red);
-    const float r = rsqrtf(ss / (float)H + eps);
-    const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-    float o[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[j] = keep ? (v[j] * r) * wv[j] : 0.f;
-    *reinterpret_cast<uint4*>(hn_out + row * H + i) =
-        make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
-  }
+  if constexpr (HN) rmsnorm_row8(v, wa, wb, rowmask == nullptr || rowmask[row] != 0, eps, H, red, hn_out + row * H + i);
 }
 
 __global__ void __launch_bounds__(256) silu_mul_k(const uint16_t* __restrict__ gu, const uint16_t* __restrict__ tab,

@@ -785,6 +785,8 @@ struct TileEntry {
   TileInfo info;
   GemmFn fn;
   GemmFn fixup = nullptr;  // persistent family: second pass over the split stream-K tiles
+  // persistent family: second pass fused with the residual RMSNorm (one workgroup per output row)
+  void (*fixup_norm)(const GemmParams, const float*, const int32_t*, float, uint16_t*) = nullptr;
 };
 
 #define OJX_TILE(BN, BM, BK, WN, WM)                                                                         \
@@ -799,7 +801,8 @@ struct TileEntry {
 // Persistent stream-K tiles: BN = WN*FN*16 W rows, BM = WM*FM*16 x rows, 64-k stages, two LDS buffers
 #define OJX_SK(FN, FM, WN, WM)                                                                               \
   {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 2 * (WN * FN * 16 + WM * FM * 16) * 128, 5},    \
-   gemm_sk_kernel<FN, FM, WN, WM>, gemm_sk_fixup_kernel<FN, FM, WN, WM>}
+   gemm_sk_kernel<FN, FM, WN, WM>, gemm_sk_fixup_kernel<FN, FM, WN, WM>,                                   \
+   gemm_sk_fixup_rmsnorm_kernel<FN, FM, WN, WM>}
 // K-interleaved pair tiles: BN = 16 FW W rows, BM = 16 (4 FX + XE) x rows, 8 waves, 64-k stages, two LDS buffers
 #define OJX_KX(FW, FX, XE)                                                                                   \
   {{16 * FW, 16 * (4 * FX + XE), 64, 4, 2, 512, (3 * 16 * FW + 2 * 16 * (4 * FX + XE)) * 128, 6},           \
@@ -929,17 +932,31 @@ hipError_t init_tiles() {
   return hipSuccess;
 }
 
-hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream, int grid) {
-  const TileEntry& e = kTiles[tile];
+static hipError_t launch_main(const TileEntry& e, int tile, int epi, const GemmParams& p, hipStream_t stream,
+                              int grid) {
   hipError_t err = set_attr(tile);
   if (err != hipSuccess) return err;
   if (grid <= 0) grid = p.tiles_n * p.tiles_m * p.splits;
   hipLaunchKernelGGL(e.fn, dim3(grid), dim3(e.info.threads), e.info.lds_bytes, stream, p, epi);
-  err = hipGetLastError();
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_residual_rmsnorm_sk(int tile, const GemmParams& p, const float* w1, const int32_t* rowmask,
+                                           float eps, uint16_t* hn_out, hipStream_t stream, int grid) {
+  const TileEntry& e = kTiles[tile];
+  if (e.fixup_norm == nullptr || p.sk_ws == nullptr || p.N % 8 != 0 || p.N / 8 > 1024) return hipErrorInvalidValue;
+  hipError_t err = launch_main(e, tile, EPI_RESID, p, stream, grid);
+  if (err != hipSuccess) return err;
+  hipLaunchKernelGGL(e.fixup_norm, dim3(p.M), dim3(p.N / 8), 0, stream, p, w1, rowmask, eps, hn_out);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream, int grid) {
+  const TileEntry& e = kTiles[tile];
+  hipError_t err = launch_main(e, tile, epi, p, stream, grid);
   if (err != hipSuccess || e.fixup == nullptr || p.sk_ws == nullptr) return err;
   const int rem = p.tiles_n * p.tiles_m - p.dp_tiles;  // the stream-K tiles
-  const int fn = e.info.bn / (16 * e.info.wn);          // one workgroup per tile and fragment column
-  hipLaunchKernelGGL(e.fixup, dim3(rem * fn), dim3(e.info.threads), 0, stream, p, epi);
+  hipLaunchKernelGGL(e.fixup, dim3(rem * (e.info.bm / 16)), dim3(256), 0, stream, p, epi);  // per 16-row block
   return hipGetLastError();
 }
 

@@ -156,6 +156,9 @@ template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_kernel(const GemmParams p, const int epi);
 template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_fixup_kernel(const GemmParams p, const int epi);
+template <int FN, int FM, int WN, int WM>
+__global__ void gemm_sk_fixup_rmsnorm_kernel(const GemmParams p, const float* w1, const int32_t* rowmask, float eps,
+                                             uint16_t* hn_out);
 // K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
 template <int FW, int FX, int XE>
 __global__ void gemm_kx_kernel(const GemmParams p, const int epi);

@@ -83,7 +83,6 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
   constexpr int GPW = (NBLK + NW - 1) / NW;     // DMA instructions per wave and stage
   constexpr int GW = BN / 8 / NW;               // of which W blocks
   static_assert((BN / 8) % NW == 0 && BM % 16 == 0, "W blocks must fill whole DMA rounds");
-  constexpr int FRAG = 256;                     // floats per 16x16 fragment in a partial slot
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];  // [2][ROWS][128 B], swizzled chunks
 
@@ -269,13 +268,15 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       // Pieces of stream-K tile ts belong to workgroups g0..g1 in K order; a workgroup keeps a tile's piece in
       // slot 2g if the tile is where its range starts, else (its range ends inside the tile) in slot 2g+1.
       // gemm_sk_fixup_kernel, launched right after this kernel, sums the pieces and applies the epilogue.
+      // A slot holds the tile row-major ([BM][BN] fp32), so that the row pass of the residual epilogue reads each
+      // row's columns contiguously.
       const int64_t x0 = (int64_t)ts * ipt;
       float* slot = p.sk_ws + (2 * L + (my0 >= x0 ? 0 : 1)) * (int64_t)(BN * BM) +
-                    (int64_t)wave * FN * FM * FRAG + lane * 4;
+                    (int64_t)(wm * FM * 16 + lr) * BN + wn * FN * 16 + lg * 4;
 #pragma unroll
       for (int i = 0; i < FN; ++i)
 #pragma unroll
-        for (int j = 0; j < FM; ++j) *reinterpret_cast<f32x4*>(slot + (i * FM + j) * FRAG) = acc[i][j];
+        for (int j = 0; j < FM; ++j) *reinterpret_cast<f32x4*>(slot + j * 16 * BN + i * 16) = acc[i][j];
       continue;
     }
 
@@ -346,20 +347,20 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams 
   else sk_body<FN, FM, WN, WM, EPI_BF16>(p);  // the host routes EPI_F32 (split-K planes) to other families
 }
 
-// Second pass of a stream-K plan, one workgroup per remaining tile and fragment column i (same waves and fragment
-// ownership as the GEMM; FN workgroups per tile, since one per tile left this pass bound by the bandwidth of a few
-// dozen CUs): a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and applies the
-// epilogue; a tile done whole by one workgroup was finished by the GEMM. The pieces are visible here because the
-// GEMM launch has ended.
+// Second pass of a stream-K plan: a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and
+// applies the epilogue; a tile done whole by one workgroup was finished by the GEMM. One workgroup of 256 threads per
+// split tile and block of 16 rows (one per tile left this pass bound by the bandwidth of a few dozen CUs); each
+// thread takes 8 consecutive columns of a row (the slots are row-major), so its loads are 32 contiguous bytes and a
+// packed gate/up group of 8 columns is whole in one thread. The pieces are visible here because the GEMM launch has
+// ended.
 template <int FN, int FM, int WN, int WM>
-__global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmParams p, const int epi) {
-  constexpr int BN = WN * FN * 16, BM = WM * FM * 16, BK = 64, FRAG = 256;
+__global__ void __launch_bounds__(256) gemm_sk_fixup_kernel(const GemmParams p, const int epi) {
+  constexpr int BN = WN * FN * 16, BM = WM * FM * 16, BK = 64, RB = BM / 16;
+  constexpr int ITEMS = 16 * BN / 8;
   __shared__ int s_slot[kSkMaxPieces];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wn = wave % WN, wm = wave / WN;
-  const int lr = lane & 15, lg = lane >> 4;
+  const int tid = threadIdx.x;
   const int ipt = (p.K + BK - 1) / BK;
-  const int ts = blockIdx.x / FN, i = blockIdx.x % FN;
+  const int ts = blockIdx.x / RB, rb = blockIdx.x % RB;
   const int64_t T = (int64_t)(p.tiles_n * p.tiles_m - p.dp_tiles) * ipt;
   const int64_t Gs = p.sk_grid;
   const int64_t x0 = (int64_t)ts * ipt;
@@ -373,21 +374,87 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_fixup_kernel(const GemmP
   __syncthreads();
   const int tau = p.dp_tiles + ts;
   const int n0 = (tau / p.tiles_m) * BN, m0 = (tau % p.tiles_m) * BM;
-  const float* base = p.sk_ws + (int64_t)wave * FN * FM * FRAG + lane * 4;
-  const float* src = base + i * FM * FRAG;
-  f32x4 v[FM];
-#pragma unroll
-  for (int j = 0; j < FM; ++j) v[j] = *reinterpret_cast<const f32x4*>(src + j * FRAG + (int64_t)s_slot[0] * (BN * BM));
-  for (int k = 1; k < np; ++k) {  // the FM loads of one piece are in flight together
-    f32x4 c[FM];
-#pragma unroll
-    for (int j = 0; j < FM; ++j) c[j] = *reinterpret_cast<const f32x4*>(src + j * FRAG + (int64_t)s_slot[k] * (BN * BM));
-#pragma unroll
-    for (int j = 0; j < FM; ++j) v[j] += c[j];
+  for (int it = tid; it < ITEMS; it += 256) {
+    const int r = rb * 16 + it / (BN / 8), c = (it % (BN / 8)) * 8;
+    const float* src = p.sk_ws + (int64_t)r * BN + c;
+    f32x4 a = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[0] * (BN * BM));
+    f32x4 b = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[0] * (BN * BM) + 4);
+    for (int k = 1; k < np; ++k) {
+      const f32x4 ca = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[k] * (BN * BM));
+      const f32x4 cb = *reinterpret_cast<const f32x4*>(src + (int64_t)s_slot[k] * (BN * BM) + 4);
+      a += ca;
+      b += cb;
+    }
+    const int m = m0 + r, n = n0 + c;
+    if (epi == EPI_SILU) {
+      store4(p, EPI_SILU, 0, m, n, true, a, b);  // columns n .. n+3 gate, n+4 .. n+7 up
+    } else {
+      store4(p, epi, 0, m, n, true, a, a);
+      store4(p, epi, 0, m, n + 4, true, b, b);
+    }
   }
+}
+
+// Second pass of a stream-K plan with the residual epilogue, fused with the RMSNorm of the rows: one workgroup per
+// output row m, N/8 threads, 8 consecutive columns each. For a column of a split tile the thread sums the tile's
+// pieces in K order exactly as gemm_sk_fixup_kernel does and writes h = bf16(residual + bf16(sum)); columns of
+// tiles done whole were written by the GEMM and are read back. Then hn = RMSNorm(h) * w1 with the arithmetic of
+// add_rmsnorm_k, so the result is bit-identical to GEMM -> fixup -> add_rmsnorm in one launch fewer, with h not
+// read back for the split tiles (the reference: bmm, then add_rmsnorm_sk2, src/fastmodel.py:196-203).
+template <int FN, int FM, int WN, int WM>
+__global__ void __launch_bounds__(1024) gemm_sk_fixup_rmsnorm_kernel(const GemmParams p, const float* w1,
+                                                                    const int32_t* rowmask, float eps,
+                                                                    uint16_t* hn_out) {
+  constexpr int BN = WN * FN * 16, BM = WM * FM * 16, BK = 64;
+  __shared__ float red[16];
+  const int m = blockIdx.x, n8 = threadIdx.x * 8;
+  const int N = p.N;
+  const int ipt = (p.K + BK - 1) / BK;
+  const int64_t T = (int64_t)(p.tiles_n * p.tiles_m - p.dp_tiles) * ipt;
+  const int64_t Gs = p.sk_grid;
+  const int tn = n8 / BN, c = n8 % BN;
+  const int tm = m / BM, mm = m % BM;
+  const int tau = tn * p.tiles_m + tm;
+  uint16_t* const h = static_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n8;
+  float v[8];
+  bool split = false;
+  int64_t g0 = 0, g1 = 0, x0 = 0;
+  if (tau >= p.dp_tiles && T > 0) {
+    x0 = (int64_t)(tau - p.dp_tiles) * ipt;
+    g0 = sk_owner(x0, T, Gs);
+    g1 = sk_owner(x0 + ipt - 1, T, Gs);
+    split = g0 != g1;
+  }
+  if (split) {
+    const float* base = p.sk_ws + (int64_t)mm * BN + c;  // row-major slots: columns c .. c+7 of tile row mm
+    auto slot = [&](int64_t g) { return (int64_t)(2 * g + (sk_start(g, T, Gs) >= x0 ? 0 : 1)) * (BN * BM); };
+    f32x4 a = *reinterpret_cast<const f32x4*>(base + slot(g0));
+    f32x4 b = *reinterpret_cast<const f32x4*>(base + slot(g0) + 4);
+    for (int64_t g = g0 + 1; g <= g1; ++g) {
+      const f32x4 ca = *reinterpret_cast<const f32x4*>(base + slot(g));
+      const f32x4 cb = *reinterpret_cast<const f32x4*>(base + slot(g) + 4);
+      a += ca;
+      b += cb;
+    }
+    const uint4 ra = *reinterpret_cast<const uint4*>(p.res + (int64_t)m * p.ldr + n8);
+    const uint32_t rw[4] = {ra.x, ra.y, ra.z, ra.w};
+    const float s[8] = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
 #pragma unroll
-  for (int j = 0; j < FM; ++j)
-    store_tile(p, epi, 0, m0 + (wm * FM + j) * 16 + lr, n0 + (wn * FN + i) * 16 + lg * 4, lg, v[j]);
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = rbf(bf2f(rw[e] & 0xffffu) + rbf(s[2 * e]));
+      v[2 * e + 1] = rbf(bf2f(rw[e] >> 16) + rbf(s[2 * e + 1]));
+    }
+    *reinterpret_cast<uint4*>(h) = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]),
+                                              pack2(v[6], v[7]));
+  } else {
+    const uint4 ha = *reinterpret_cast<const uint4*>(h);
+    const uint32_t hw[4] = {ha.x, ha.y, ha.z, ha.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { v[2 * e] = bf2f(hw[e] & 0xffffu); v[2 * e + 1] = bf2f(hw[e] >> 16); }
+  }
+  (void)N;
+  const float4 wa = *reinterpret_cast<const float4*>(w1 + n8), wb = *reinterpret_cast<const float4*>(w1 + n8 + 4);
+  rmsnorm_row8(v, wa, wb, rowmask == nullptr || rowmask[m] != 0, eps, p.N, red, hn_out + (int64_t)m * p.N + n8);
 }
 
 }  // namespace ojx
@@ -396,16 +463,30 @@ namespace ojx {
 // Tile shapes of this family (registered in gemm.hip's tile table): BN x BM = (WN*FN*16) x (WM*FM*16).
 template __global__ void gemm_sk_kernel<8, 4, 2, 4>(const GemmParams, const int);  // 256 x 256
 template __global__ void gemm_sk_fixup_kernel<8, 4, 2, 4>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<8, 4, 2, 4>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<4, 9, 4, 2>(const GemmParams, const int);  // 256 x 288
 template __global__ void gemm_sk_fixup_kernel<4, 9, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<4, 9, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<4, 4, 4, 2>(const GemmParams, const int);  // 256 x 128
 template __global__ void gemm_sk_fixup_kernel<4, 4, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<4, 4, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<4, 6, 4, 2>(const GemmParams, const int);  // 256 x 192
 template __global__ void gemm_sk_fixup_kernel<4, 6, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<4, 6, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<4, 3, 4, 2>(const GemmParams, const int);  // 256 x 96
 template __global__ void gemm_sk_fixup_kernel<4, 3, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<4, 3, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<2, 9, 4, 2>(const GemmParams, const int);  // 128 x 288
 template __global__ void gemm_sk_fixup_kernel<2, 9, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<2, 9, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 template __global__ void gemm_sk_kernel<3, 9, 4, 2>(const GemmParams, const int);  // 192 x 288
 template __global__ void gemm_sk_fixup_kernel<3, 9, 4, 2>(const GemmParams, const int);
+template __global__ void gemm_sk_fixup_rmsnorm_kernel<3, 9, 4, 2>(const GemmParams, const float*, const int32_t*,
+                                                                  float, uint16_t*);
 }  // namespace ojx

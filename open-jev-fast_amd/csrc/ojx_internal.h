@@ -22,6 +22,39 @@ __device__ __forceinline__ float rbf(float f) { return bf2f(f2bf(f)); }  // roun
 __device__ __forceinline__ float silu_f(float x) { return x / (1.0f + expf(-x)); }
 __device__ __forceinline__ float sigmoid_f(float x) { return 1.0f / (1.0f + expf(-x)); }
 
+__device__ __forceinline__ uint32_t pack2(float a, float b) { return f2bf(a) | (f2bf(b) << 16); }
+
+// Sum over the whole workgroup (wave64 butterfly, then one value per wave through LDS).
+__device__ __forceinline__ float block_sum(float v, float* red) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6, nw = (blockDim.x + 63) >> 6;
+  if (lane == 0) red[wid] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int i = 0; i < nw; ++i) t += red[i];
+  return t;
+}
+
+// RMSNorm of one row held by one workgroup of H/8 threads, 8 consecutive elements v[] per thread (the bf16-rounded
+// h as floats): hn = bf16((h * rsqrt(sum h^2 / H + eps)) * w1), zero on a masked row (reference: add_rmsnorm_k,
+// src/kernels.cu:41-73). Each thread sums its own 8 squares in order, then block_sum: every kernel that normalises
+// a row this way gets the same bits.
+__device__ __forceinline__ void rmsnorm_row8(const float (&v)[8], float4 wa, float4 wb, bool keep, float eps, int H,
+                                             float* red, uint16_t* hn_dst) {
+  float ss = 0.f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ss += v[j] * v[j];
+  ss = block_sum(ss, red);
+  const float r = rsqrtf(ss / (float)H + eps);
+  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) o[j] = keep ? (v[j] * r) * wv[j] : 0.f;
+  *reinterpret_cast<uint4*>(hn_dst) =
+      make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+}
+
 // ----------------------------------------------------------------------------------------------------------------
 // GEMM epilogue modes (what a workgroup does with its fp32 accumulator tile)
 enum Epi : int {
@@ -63,6 +96,10 @@ hipError_t init_tiles();  // sets the dynamic-LDS limit of every tile kernel
 const TileInfo* tile_info(int tile);
 // grid: workgroups to launch; 0 = one per (tile, split) (the persistent family passes its own)
 hipError_t launch_gemm(int tile, int epi, const GemmParams& p, hipStream_t stream, int grid = 0);
+// Persistent family with a residual epilogue and split tiles: the GEMM (without its split-tile pass), then one
+// launch per output row that sums the split tiles' pieces, adds the residual (h) and normalises the row (hn).
+hipError_t launch_gemm_residual_rmsnorm_sk(int tile, const GemmParams& p, const float* w1, const int32_t* rowmask,
+                                           float eps, uint16_t* hn_out, hipStream_t stream, int grid);
 
 // Row / elementwise kernels (epilogue.hip)
 hipError_t launch_reduce_bf16(const float* parts, int S, int64_t part_stride, uint16_t* y, int64_t ldy,

@@ -396,6 +396,31 @@ def test_stream_k_epilogues_ragged_m(pkg, ext, O, dev, M):
             _assert_tol(O, hn, rhn, f"hn M {M} tile {t} S {S}")
 
 
+@pytest.mark.parametrize("M,N,K", [(288, 5120, 2176), (539, 1024, 640), (7, 2048, 1024)])
+def test_stream_k_residual_row_pass_bitexact(pkg, ext, O, dev, M, N, K):
+    """Persistent residual plans with split tiles run the GEMM and then one row pass that sums the split tiles,
+    adds the residual and normalises (two launches). It must equal, bit for bit, the GEMM + split-tile pass without
+    the norm followed by the standalone add_rmsnorm on h, and match the oracle."""
+    g = torch.Generator().manual_seed(M + N)
+    x = torch.randn(M, K, generator=g).bfloat16()
+    w = (torch.randn(N, K, generator=g) * 0.02).bfloat16()
+    res = torch.randn(M, N, generator=g).bfloat16()
+    w1 = (1.0 + 0.1 * torch.randn(N, generator=g)).float()
+    mask = (torch.rand(M, generator=g) > 0.25).int()
+    rh, rhn = O.residual_proj(res, x, w, w1, mask, 1e-6, S=1)
+    xd, wd, rd, w1d, md = x.to(dev), w.to(dev), res.to(dev), w1.to(dev), mask.to(dev)
+    for t in _sk_tiles(pkg):
+        for S in (2, 4, 8):
+            _say(f"case stream-K residual row pass M={M} N={N} K={K} tile={t} S={S}")
+            h, hn = ext.mm_residual_rmsnorm(rd, xd, wd, w1d, md, 1e-6, cfg=(t, S))
+            h0, _ = ext.mm_residual_rmsnorm(rd, xd, wd, w1d, md, 1e-6, want_hn=False, cfg=(t, S))
+            _, hn0 = ext.add_rmsnorm(h0, None, w1d, md, 1e-6)
+            assert torch.equal(h, h0), f"tile {t} S {S}: h differs from GEMM + split-tile pass"
+            assert torch.equal(hn, hn0), f"tile {t} S {S}: hn differs from add_rmsnorm of h"
+            _assert_tol(O, h, rh, f"h tile {t} S {S}")
+            _assert_tol(O, hn, rhn, f"hn tile {t} S {S}")
+
+
 def test_bf16_rounding_bit_patterns(ext, dev):
     """Every fp32 -> bf16 rounding in the kernels (one hardware conversion) is round-to-nearest-even, checked
     bit-exactly against torch's CPU conversion on about a million fp32 bit patterns: random words, the three
