@@ -900,6 +900,10 @@ static const TileEntry kTiles[] = {
     OJX_KX(8, 4, 2),                // 81 128 x 288
     OJX_KX(9, 2, 1),                // 82 144 x 144
     OJX_KX(8, 4, 0),                // 83 128 x 256
+    OJX_KX(9, 1, 0),                // 84 144 x 64: M <= 64, 242 W tiles of the gate-up
+    OJX_KX(9, 2, 0),                // 85 144 x 128
+    OJX_KX(8, 2, 0),                // 86 128 x 128
+    OJX_KX(8, 1, 0),                // 87 128 x 64
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

@@ -292,5 +292,9 @@ template __global__ void gemm_kx_kernel<9, 4, 2>(const GemmParams, const int);  
 template __global__ void gemm_kx_kernel<8, 4, 2>(const GemmParams, const int);  // 128 x 288
 template __global__ void gemm_kx_kernel<9, 2, 1>(const GemmParams, const int);  // 144 x 144
 template __global__ void gemm_kx_kernel<8, 4, 0>(const GemmParams, const int);  // 128 x 256
+template __global__ void gemm_kx_kernel<9, 1, 0>(const GemmParams, const int);  // 144 x 64
+template __global__ void gemm_kx_kernel<9, 2, 0>(const GemmParams, const int);  // 144 x 128
+template __global__ void gemm_kx_kernel<8, 2, 0>(const GemmParams, const int);  // 128 x 128
+template __global__ void gemm_kx_kernel<8, 1, 0>(const GemmParams, const int);  // 128 x 64
 
 }  // namespace ojx
