@@ -38,7 +38,8 @@ enum {
 enum {
   OJX_KIND_PLAIN = 0,     /* y = x W^T */
   OJX_KIND_SILU_MUL = 1,  /* gate-up projection with the SiLU(gate) * up epilogue */
-  OJX_KIND_RESIDUAL = 2   /* out / o_proj / down projection with residual add (+ RMSNorm) */
+  OJX_KIND_RESIDUAL = 2,  /* out / o_proj / down projection with residual add (+ RMSNorm) */
+  OJX_KIND_PACKED = 4     /* or-ed into a kind: the weight is in the ojx_pack_weight layout (the *_pk entry points) */
 };
 
 /* One kernel configuration: a tile shape from the tile registry and a split-K count. Optionally the last
@@ -115,6 +116,27 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
                               const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
                               int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
                               ojx_stream_t stream);
+
+/* Load-time weight layout: W [N, K] row-major -> wp [K/64][N/16][16][64] bf16 (N % 16 == 0, K % 64 == 0, at most
+ * 2 GiB). The 16-row x 64-k blocks of one 64-k stage of all rows are contiguous, so the weights a workgroup streams
+ * for one stage of its tile are one contiguous run instead of one 128-byte piece per row (measured on MI355X: a
+ * weight stream of 144-row tiles reads 6.8 TB/s against 6.5 row-major). For the fused gate-up, pack the output of
+ * ojx_pack_gate_up. Replaces the load-time weight re-layout of _split (src/fastmodel.py:86-112, 186-188) with one
+ * copy in a layout the kernels stream; the row-major W is no longer needed once packed. */
+int ojx_pack_weight(const void* w, void* wp, int64_t N, int64_t K, ojx_stream_t stream);
+
+/* ojx_gemm_bf16 / ojx_gemm_silu_mul / ojx_gemm_residual_rmsnorm on a packed weight: same arguments and results (x
+ * row-major as before), the weight in the ojx_pack_weight layout. Tile families 0, 5 and 6 read it; cfg NULL = the
+ * plan for kind | OJX_KIND_PACKED; an explicit cfg must name a tile of those families, with no tail, and split-K
+ * chunks are whole 64-k stages (ceil(K / S) rounded up to a multiple of 64). */
+int ojx_gemm_bf16_pk(const void* x, const void* wp, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                     int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream);
+int ojx_gemm_silu_mul_pk(const void* x, const void* w_gu_pk, void* out, int64_t M, int64_t I, int64_t K,
+                         void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream);
+int ojx_gemm_residual_rmsnorm_pk(const void* x, const void* wp, const void* residual, const float* w1,
+                                 const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
+                                 int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                                 ojx_stream_t stream);
 
 /* Bytes of the static device scratch behind ojx_gemm_residual_rmsnorm_noalloc (one array per GPU). */
 #define OJX_NOALLOC_SCRATCH_BYTES (32LL << 20)

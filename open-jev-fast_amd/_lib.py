@@ -46,6 +46,11 @@ EXPORTS = {
                                                  _cfgp, _p]),
     "ojx_gemm_residual_rmsnorm_noalloc": (ctypes.c_int, [_p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _i64, _cfgp,
                                                          _p]),
+    "ojx_pack_weight": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
+    "ojx_gemm_bf16_pk": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _cfgp, _p]),
+    "ojx_gemm_silu_mul_pk": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _cfgp, _p]),
+    "ojx_gemm_residual_rmsnorm_pk": (ctypes.c_int, [_p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _i64, _p, _i64,
+                                                    _cfgp, _p]),
     "ojx_add_rmsnorm": (ctypes.c_int, [_p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _p]),
     "ojx_add_rmsnorm_sk": (ctypes.c_int, [_p, _p, _i32, _p, _p, _f32, _p, _p, _i64, _i64, _p]),
     "ojx_silu_mul": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
@@ -55,7 +60,7 @@ EXPORTS = {
     "ojx_pack_gate_up": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _p]),
 }
 
-KIND_PLAIN, KIND_SILU_MUL, KIND_RESIDUAL = 0, 1, 2
+KIND_PLAIN, KIND_SILU_MUL, KIND_RESIDUAL, KIND_PACKED = 0, 1, 2, 4
 
 _lib = None
 

@@ -32,6 +32,9 @@ int hip_check(hipError_t e, const char* what) {
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 inline int64_t kchunk_for(int64_t K, int64_t S) { return cdiv(cdiv(K, S), 8) * 8; }
+// split-K chunk over a packed weight: whole 64-k stages
+inline int64_t kchunk_pk(int64_t K, int64_t S) { return cdiv(cdiv(K, S), 64) * 64; }
+inline bool is_packed_kind(int32_t kind) { return (kind & OJX_KIND_PACKED) != 0; }
 
 struct PlanEntry {
   int64_t M, N, K;
@@ -102,8 +105,24 @@ bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
   return (splitk - 1) * ch < K;  // every split owns a non-empty K range
 }
 
-bool cfg_fits(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
+// A packed weight is read by the K-interleaved family only, without tails, with splits of whole 64-k stages.
+// Tile families that read the packed layout: 0 (both operands through registers and LDS), 5 (persistent) and 6.
+bool reads_packed(int32_t tile) {
+  const ojx::TileInfo* t = ojx::tile_info(tile);
+  return t != nullptr && (t->family == 0 || t->family == 5 || t->family == 6);
+}
+
+// A packed weight: no tails, splits of whole 64-k stages (the persistent family's splitk is its stream-K spread).
+bool cfg_fits_packed(int64_t N, int64_t K, const ojx_cfg& c) {
+  if (!reads_packed(c.tile) || c.tail_rows != 0 || c.splitk < 1 || c.splitk > kMaxSplit) return false;
+  if (N % 16 != 0 || K % 64 != 0 || N * K * 2 >= (1LL << 31)) return false;
+  if (is_sk(c.tile)) return true;
+  return (c.splitk - 1) * kchunk_pk(K, c.splitk) < K;
+}
+
+bool cfg_fits(int64_t M, int64_t N, int64_t K, const ojx_cfg& c, bool packed = false) {
   (void)M;
+  if (packed) return cfg_fits_packed(N, K, c);
   if (!part_fits(K, c.tile, c.splitk)) return false;
   if (c.tail_rows == 0) return true;
   return c.tail_rows > 0 && c.tail_rows < N && c.tail_rows % 8 == 0 && part_fits(K, c.tail_tile, c.tail_splitk);
@@ -138,8 +157,17 @@ int64_t workspace_for(const ojx_cfg& c, int64_t M, int64_t N, int64_t K) {
 }
 
 ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
-  (void)kind;
   ojx_cfg c{};
+  if (is_packed_kind(kind)) {  // skinny tile, K-interleaved tile or persistent tile for the M range
+    c.tile = M <= 16 ? 0 : M <= 64 ? 84 : M <= 128 ? 85 : M <= 288 ? 80 : 73;
+    const ojx::TileInfo* t = ojx::tile_info(c.tile);
+    const int64_t tiles = cdiv(N, t->bn) * cdiv(M, t->bm);
+    int64_t S = 1;
+    while (S < 8 && tiles * S * 2 <= 320 && K / (S * 2) >= 512) S *= 2;
+    c.splitk = (int32_t)S;
+    while (c.splitk > 1 && !cfg_fits_packed(N, K, c)) --c.splitk;
+    return c;
+  }
   if (M <= 16) c.tile = 0;
   else if (M <= 32) c.tile = 2;
   else if (M <= 64) c.tile = 4;
@@ -156,7 +184,7 @@ ojx_cfg heuristic_plan(int64_t M, int64_t N, int64_t K, int32_t kind) {
 
 int resolve(int64_t M, int64_t N, int64_t K, int32_t kind, const ojx_cfg* cfg, ojx_cfg* out) {
   if (cfg != nullptr) {
-    if (!cfg_fits(M, N, K, *cfg))
+    if (!cfg_fits(M, N, K, *cfg, is_packed_kind(kind)))
       return fail(OJX_ERR_CONFIG, "config (tile %d, splitk %d, tail %d/%d/%d) invalid for M=%lld N=%lld K=%lld",
                   cfg->tile, cfg->splitk, cfg->tail_tile, cfg->tail_splitk, cfg->tail_rows, (long long)M,
                   (long long)N, (long long)K);
@@ -182,7 +210,7 @@ int check_dims(int64_t M, int64_t N, int64_t K) {
 int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
          const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st, void* ws = nullptr,
          int64_t ws_off = 0, const float* w1 = nullptr, const int32_t* rowmask = nullptr, float eps = 0.f,
-         uint16_t* hn_out = nullptr) {
+         uint16_t* hn_out = nullptr, bool packed = false) {
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
   ojx::GemmParams p;
   p.W = static_cast<const uint16_t*>(w);
@@ -197,7 +225,8 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
-  p.kchunk = (int)kchunk_for(K, c.splitk);
+  p.kchunk = (int)(packed ? kchunk_pk(K, c.splitk) : kchunk_for(K, c.splitk));
+  p.wpk = packed ? 1 : 0;
   p.tiles_n = (int)cdiv(N, t->bn);
   p.tiles_m = (int)cdiv(M, t->bm);
   p.splits = c.splitk;
@@ -311,21 +340,24 @@ int ojx_tile_info(int32_t tile, int32_t* info7) {
 
 int ojx_plan(int64_t M, int64_t N, int64_t K, int32_t kind, ojx_cfg* out) {
   if (out == nullptr) return fail(OJX_ERR_ARG, "null plan output");
-  if (kind < OJX_KIND_PLAIN || kind > OJX_KIND_RESIDUAL) return fail(OJX_ERR_ARG, "unknown kind %d", kind);
+  const int32_t base = kind & ~OJX_KIND_PACKED;
+  if (base < OJX_KIND_PLAIN || base > OJX_KIND_RESIDUAL || (kind & ~(OJX_KIND_PACKED | 3)) != 0)
+    return fail(OJX_ERR_ARG, "unknown kind %d", kind);
+  const bool packed = is_packed_kind(kind);
   for (const PlanEntry& e : kPlan) {
     if (e.M == M && e.N == N && e.K == K && e.kind == kind) {
       ojx_cfg c{e.tile, e.splitk, e.tail_tile, e.tail_splitk, e.tail_rows};
       if (c.tail_splitk == 0) c.tail_splitk = 1;
-      if (cfg_fits(M, N, K, c)) { *out = c; return OJX_OK; }
+      if (cfg_fits(M, N, K, c, packed)) { *out = c; return OJX_OK; }
     }
   }
   *out = heuristic_plan(M, N, K, kind);
-  if (!cfg_fits(M, N, K, *out)) *out = ojx_cfg{out->tile, 1, 0, 1, 0};
+  if (!cfg_fits(M, N, K, *out, packed)) *out = ojx_cfg{out->tile, 1, 0, 1, 0};
   return OJX_OK;
 }
 
-static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
-  if (!cfg_fits(M, N, K, c)) return false;
+static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c, bool packed) {
+  if (!cfg_fits(M, N, K, c, packed)) return false;
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
   const int64_t mp = cdiv(M > 0 ? M : 1, 16) * 16;
   if (t->bm >= 2 * mp) return false;                   // more than half the x tile would be padding
@@ -334,20 +366,20 @@ static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c) {
 }
 
 int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind) {
-  (void)kind;
+  const bool packed = is_packed_kind(kind);
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
-    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}) ? 1 : 0;
+    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}, packed) ? 1 : 0;
   return n;
 }
 
 int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, ojx_cfg* out) {
-  (void)kind;
+  const bool packed = is_packed_kind(kind);
   if (out == nullptr) return fail(OJX_ERR_ARG, "null candidate output");
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
     for (int s : kSplits)
-      if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0})) {
+      if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}, packed)) {
         if (n == idx) { *out = ojx_cfg{t, s, 0, 1, 0}; return OJX_OK; }
         ++n;
       }
@@ -358,37 +390,6 @@ int64_t ojx_workspace_bytes(int64_t M, int64_t N, int64_t K, int32_t kind, const
   ojx_cfg c{};
   if (resolve(M, N, K, kind, cfg, &c) != OJX_OK) return -1;
   return workspace_for(c, M, N, K);
-}
-
-int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
-                  int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
-                  ojx_stream_t stream) {
-  OJX_TRY(check_dims(M, N, K));
-  if (M == 0) return OJX_OK;  // an empty tensor may have a null data pointer
-  OJX_TRY(check_operands(x, w, ldx, ldw, K));
-  if (y == nullptr || !aligned(y, 8) || ldy < N || ldy % 4 != 0)
-    return fail(OJX_ERR_ARG, "y must be 8-byte aligned with row stride >= N and a multiple of 4");
-  ojx_cfg c{};
-  OJX_TRY(resolve(M, N, K, OJX_KIND_PLAIN, cfg, &c));
-  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  Part parts[2];
-  const int np = split_parts(c, M, N, K, parts);
-  for (int i = 0; i < np; ++i) {
-    const Part& q = parts[i];
-    const void* wq = static_cast<const uint16_t*>(w) + q.n0 * ldw;
-    uint16_t* yq = static_cast<uint16_t*>(y) + q.n0;
-    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
-      OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st,
-                   workspace, q.ws));
-      continue;
-    }
-    float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
-    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, ldx, wq, ldw, pp, q.n, nullptr, 0, M, q.n, K, st));
-    OJX_TRY(hip_check(ojx::launch_reduce_bf16(pp, q.c.splitk, M * q.n, yq, ldy, (int)M, (int)q.n, st),
-                      "reduce launch"));
-  }
-  return OJX_OK;
 }
 
 int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, int64_t N, int64_t K, int64_t ldx,
@@ -412,8 +413,43 @@ int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, i
   return gemm(c, ojx::EPI_F32, x, ldx, w, ldw, parts, N, nullptr, 0, M, N, K, static_cast<hipStream_t>(stream));
 }
 
-int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t M, int64_t I, int64_t K,
-                      void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
+}  // extern "C"
+
+static int gemm_bf16_impl(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                          int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                          ojx_stream_t stream, bool packed) {
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;  // an empty tensor may have a null data pointer
+  OJX_TRY(check_operands(x, w, ldx, ldw, K));
+  if (y == nullptr || !aligned(y, 8) || ldy < N || ldy % 4 != 0)
+    return fail(OJX_ERR_ARG, "y must be 8-byte aligned with row stride >= N and a multiple of 4");
+  ojx_cfg c{};
+  OJX_TRY(resolve(M, N, K, OJX_KIND_PLAIN | (packed ? OJX_KIND_PACKED : 0), cfg, &c));
+  OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  Part parts[2];
+  const int np = split_parts(c, M, N, K, parts);
+  for (int i = 0; i < np; ++i) {
+    const Part& q = parts[i];
+    const void* wq = static_cast<const uint16_t*>(w) + q.n0 * ldw;
+    uint16_t* yq = static_cast<uint16_t*>(y) + q.n0;
+    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
+      OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st,
+                   workspace, q.ws, nullptr, nullptr, 0.f, nullptr, packed));
+      continue;
+    }
+    float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
+    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, ldx, wq, ldw, pp, q.n, nullptr, 0, M, q.n, K, st, nullptr, 0, nullptr,
+                 nullptr, 0.f, nullptr, packed));
+    OJX_TRY(hip_check(ojx::launch_reduce_bf16(pp, q.c.splitk, M * q.n, yq, ldy, (int)M, (int)q.n, st),
+                      "reduce launch"));
+  }
+  return OJX_OK;
+}
+
+static int gemm_silu_mul_impl(const void* x, const void* w_gu_packed, void* out, int64_t M, int64_t I, int64_t K,
+                              void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream,
+                              bool packed) {
   if (I <= 0 || I % 4 != 0) return fail(OJX_ERR_SHAPE, "I (%lld) must be a positive multiple of 4", (long long)I);
   const int64_t N = 2 * I;
   OJX_TRY(check_dims(M, N, K));
@@ -421,7 +457,7 @@ int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t
   OJX_TRY(check_operands(x, w_gu_packed, K, K, K));
   if (out == nullptr || !aligned(out, 8)) return fail(OJX_ERR_ARG, "out must be 8-byte aligned");
   ojx_cfg c{};
-  OJX_TRY(resolve(M, N, K, OJX_KIND_SILU_MUL, cfg, &c));
+  OJX_TRY(resolve(M, N, K, OJX_KIND_SILU_MUL | (packed ? OJX_KIND_PACKED : 0), cfg, &c));
   OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
   hipStream_t st = static_cast<hipStream_t>(stream);
   Part parts[2];
@@ -432,21 +468,22 @@ int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t
     uint16_t* oq = static_cast<uint16_t*>(out) + q.n0 / 2;  // packed blocks of 8 rows give 4 output columns
     if (q.c.splitk == 1 || is_sk(q.c.tile)) {
       OJX_TRY(gemm(q.c, ojx::EPI_SILU, x, K, wq, K, oq, I, nullptr, 0, M, q.n, K, st,
-                   workspace, q.ws));
+                   workspace, q.ws, nullptr, nullptr, 0.f, nullptr, packed));
       continue;
     }
     float* pp = reinterpret_cast<float*>(static_cast<char*>(workspace) + q.ws);
-    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, K, wq, K, pp, q.n, nullptr, 0, M, q.n, K, st));
+    OJX_TRY(gemm(q.c, ojx::EPI_F32, x, K, wq, K, pp, q.n, nullptr, 0, M, q.n, K, st, nullptr, 0, nullptr, nullptr,
+                 0.f, nullptr, packed));
     OJX_TRY(hip_check(ojx::launch_reduce_silu(pp, q.c.splitk, M * q.n, oq, I, (int)M, (int)q.n, st),
                       "reduce launch"));
   }
   return OJX_OK;
 }
 
-int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual, const float* w1,
-                              const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
-                              int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
-                              ojx_stream_t stream) {
+static int gemm_residual_rmsnorm_impl(const void* x, const void* w, const void* residual, const float* w1,
+                                      const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M,
+                                      int64_t N, int64_t K, void* workspace, int64_t workspace_bytes,
+                                      const ojx_cfg* cfg, ojx_stream_t stream, bool packed) {
   OJX_TRY(check_dims(M, N, K));
   if (M == 0) return OJX_OK;
   OJX_TRY(check_operands(x, w, K, K, K));
@@ -459,7 +496,7 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   }
   if (M == 0) return OJX_OK;
   ojx_cfg c{};
-  OJX_TRY(resolve(M, N, K, OJX_KIND_RESIDUAL, cfg, &c));
+  OJX_TRY(resolve(M, N, K, OJX_KIND_RESIDUAL | (packed ? OJX_KIND_PACKED : 0), cfg, &c));
   if (c.tail_rows != 0)
     return fail(OJX_ERR_CONFIG, "tail configurations apply to the plain and SiLU.mul GEMMs only (the RMSNorm "
                                 "epilogue needs whole rows)");
@@ -472,9 +509,10 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
       // persistent plan with split tiles: GEMM, then one launch that sums the pieces, adds the residual and
       // normalises each row
       return gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, w1, rowmask,
-                  eps, hn);
+                  eps, hn, packed);
     }
-    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0));
+    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, nullptr, nullptr,
+                 0.f, nullptr, packed));
     if (hn == nullptr) return OJX_OK;
     return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,
                                              (int)N, st), "rmsnorm launch");
@@ -482,9 +520,69 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
   if (hn == nullptr && N / 8 > 1024) return fail(OJX_ERR_SHAPE, "split-K residual needs N/8 <= 1024");
   OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
   float* parts = static_cast<float*>(workspace);
-  OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st));
+  OJX_TRY(gemm(c, ojx::EPI_F32, x, K, w, K, parts, N, nullptr, 0, M, N, K, st, nullptr, 0, nullptr, nullptr, 0.f,
+               nullptr, packed));
   return hip_check(ojx::launch_add_rmsnorm(static_cast<const uint16_t*>(residual), nullptr, parts, c.splitk, M * N,
                                            w1, rowmask, eps, h, hn, (int)M, (int)N, st), "rmsnorm launch");
+}
+
+extern "C" {
+
+int ojx_gemm_bf16(const void* x, const void* w, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                  int64_t ldw, int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                  ojx_stream_t stream) {
+  return gemm_bf16_impl(x, w, y, M, N, K, ldx, ldw, ldy, workspace, workspace_bytes, cfg, stream, false);
+}
+
+int ojx_gemm_silu_mul(const void* x, const void* w_gu_packed, void* out, int64_t M, int64_t I, int64_t K,
+                      void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
+  return gemm_silu_mul_impl(x, w_gu_packed, out, M, I, K, workspace, workspace_bytes, cfg, stream, false);
+}
+
+int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual, const float* w1,
+                              const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
+                              int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                              ojx_stream_t stream) {
+  return gemm_residual_rmsnorm_impl(x, w, residual, w1, rowmask, eps, h_out, hn_out, M, N, K, workspace,
+                                    workspace_bytes, cfg, stream, false);
+}
+
+static int check_packed_shape(int64_t N, int64_t K) {
+  if (N % 16 != 0 || K % 64 != 0)
+    return fail(OJX_ERR_SHAPE, "packed weights need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
+                (long long)K);
+  if (N * K * 2 >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "packed weight larger than 2 GiB");
+  return OJX_OK;
+}
+
+int ojx_pack_weight(const void* w, void* wp, int64_t N, int64_t K, ojx_stream_t stream) {
+  OJX_TRY(check_dims(1, N, K));
+  OJX_TRY(check_packed_shape(N, K));
+  if (w == nullptr || wp == nullptr || !aligned(w, 16) || !aligned(wp, 16))
+    return fail(OJX_ERR_ARG, "w and wp must be non-null and 16-byte aligned");
+  return hip_check(ojx::launch_pack_weight(static_cast<const uint16_t*>(w), static_cast<uint16_t*>(wp), N, K,
+                                           static_cast<hipStream_t>(stream)), "pack launch");
+}
+
+int ojx_gemm_bf16_pk(const void* x, const void* wp, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
+                     int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
+  OJX_TRY(check_packed_shape(N, K));
+  return gemm_bf16_impl(x, wp, y, M, N, K, ldx, K, ldy, workspace, workspace_bytes, cfg, stream, true);
+}
+
+int ojx_gemm_silu_mul_pk(const void* x, const void* w_gu_pk, void* out, int64_t M, int64_t I, int64_t K,
+                         void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
+  OJX_TRY(check_packed_shape(2 * I, K));
+  return gemm_silu_mul_impl(x, w_gu_pk, out, M, I, K, workspace, workspace_bytes, cfg, stream, true);
+}
+
+int ojx_gemm_residual_rmsnorm_pk(const void* x, const void* wp, const void* residual, const float* w1,
+                                 const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M, int64_t N,
+                                 int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
+                                 ojx_stream_t stream) {
+  OJX_TRY(check_packed_shape(N, K));
+  return gemm_residual_rmsnorm_impl(x, wp, residual, w1, rowmask, eps, h_out, hn_out, M, N, K, workspace,
+                                    workspace_bytes, cfg, stream, true);
 }
 
 int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* residual, const float* w1,

@@ -165,6 +165,19 @@ __global__ void __launch_bounds__(256) pack_gate_up_k(const uint16_t* __restrict
   *reinterpret_cast<uint4*>(packed + p * K + c) = *reinterpret_cast<const uint4*>(src);
 }
 
+// W row n, 8 columns k .. k+7 (k % 8 == 0) -> the packed layout: stage s = k / 64, row block nb = n / 16, offset
+// ((s * N / 16 + nb) * 16 + n % 16) * 64 + k % 64. One thread per 16 bytes; reads and writes are both contiguous
+// runs (a row's 128 bytes of one stage land in one 128-byte line of the packed buffer).
+__global__ void __launch_bounds__(256) pack_weight_k(const uint16_t* __restrict__ w, uint16_t* __restrict__ wp,
+                                                     int64_t N, int64_t K) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t cpr = K >> 3;
+  if (idx >= N * cpr) return;
+  const int64_t n = idx / cpr, k = (idx - n * cpr) * 8;
+  const int64_t dst = (((k >> 6) * (N >> 4) + (n >> 4)) * 16 + (n & 15)) * 64 + (k & 63);
+  *reinterpret_cast<uint4*>(wp + dst) = *reinterpret_cast<const uint4*>(w + n * K + k);
+}
+
 static inline unsigned nblocks(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
 // Scoring head (src/server.py:37,57,129: mdl.head(hn[lastidx].float()).squeeze(-1), a Linear(H, 1) on fp32):
@@ -253,6 +266,11 @@ hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_
                                hipStream_t st) {
   const int64_t n = (int64_t)2 * I * (K / 8);
   hipLaunchKernelGGL(pack_gate_up_k, dim3(nblocks(n, 256)), dim3(256), 0, st, gate, up, packed, I, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_pack_weight(const uint16_t* w, uint16_t* wp, int64_t N, int64_t K, hipStream_t st) {
+  hipLaunchKernelGGL(pack_weight_k, dim3(nblocks(N * (K / 8), 256)), dim3(256), 0, st, w, wp, N, K);
   return hipGetLastError();
 }
 

@@ -59,9 +59,13 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
   const int ke = min(p.K, kb + p.kchunk);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
-  // descriptors cover this tile's rows only: rows past N (or M) read zeros
-  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  // descriptors cover this tile's rows only: rows past N (or M) read zeros. A packed W ([K/64][N/16][16][64], see
+  // ojx_pack_weight) goes through one descriptor over the whole buffer, rows past N skipped.
+  const bool wpk = p.wpk != 0;
+  const __amdgpu_buffer_rsrc_t rsW = wpk ? make_rsrc(p.W, (int64_t)p.N * p.K * 2)
+                                         : make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
   const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
+  const int nbw = p.N >> 4;
   uint4 rw[CW], rx[CX];
   auto gload = [&](int k0) {
 #pragma unroll
@@ -69,7 +73,16 @@ __global__ void __launch_bounds__(64 * WN * WM) gemm_nt_kernel(const GemmParams 
       const int c = tid + i * NT;
       const int row = c / CPR, col = (c % CPR) * 8;
       const bool ok = (W_CH % NT == 0 || c < W_CH) && k0 + col < ke;
-      rw[i] = bload_nt(rsW, ok ? (uint32_t)(row * p.ldw + k0 + col) * 2u : kOOB);
+      uint32_t o;
+      bool okw = ok;
+      if (wpk) {
+        const int n = n0 + row, k = k0 + col;
+        o = (uint32_t)(((((k >> 6) * nbw + (n >> 4)) * 16 + (n & 15)) * 64 + (k & 63)) * 2);
+        okw = ok && n < p.N;
+      } else {
+        o = (uint32_t)(row * p.ldw + k0 + col) * 2u;
+      }
+      rw[i] = bload_nt(rsW, okw ? o : kOOB);
     }
 #pragma unroll
     for (int i = 0; i < CX; ++i) {

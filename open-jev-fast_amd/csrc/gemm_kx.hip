@@ -76,7 +76,10 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   const int ke = min(p.K, kb + p.kchunk);
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
-  const __amdgpu_buffer_rsrc_t rsW = make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  // row-major W: this tile's rows only (rows past N read zeros); packed W: the whole buffer, blocks past N skipped
+  const __amdgpu_buffer_rsrc_t rsW = p.wpk ? make_rsrc(p.W, (int64_t)p.N * p.K * 2)
+                                           : make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
+  const int nbw = p.N >> 4;  // 16-row blocks of the packed W
   const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
 
   // ------------------------------------------------------------------ fragment ownership
@@ -116,12 +119,13 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   // offsets for an even and an odd block (the swizzle depends on the block's parity); the block's own part is
   // wave-uniform and computed at issue.
   int kcp[2];
-  uint32_t lx[2], lw[2];
+  uint32_t lx[2], lw[2], lpk[2];
 #pragma unroll
   for (int par = 0; par < 2; ++par) {
     kcp[par] = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;
     lx[par] = (uint32_t)(((lane >> 3) * p.ldx + kcp[par]) * 2);
     lw[par] = (uint32_t)(((lane >> 3) * p.ldw + kcp[par]) * 2);
+    lpk[par] = (uint32_t)(((lane >> 3) * 64 + kcp[par]) * 2);  // packed: rows of 128 bytes
   }
   // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
   auto dma = [&](int st, int lo, int hi) {
@@ -134,8 +138,16 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
       const int blk = isw ? c - XB : c, par = blk & 1;
       const bool ok = st < nk && k0 + kcp[par] < ke;
       if (isw) {
-        const uint32_t o = (uint32_t)(blk * 8 * p.ldw * 2) + lw[par] + (uint32_t)k0 * 2u;
-        dma16_nt(rsW, wring + (st % S::WD) * WST + blk * 1024, ok ? o : kOOB);
+        uint32_t o;
+        bool okw = ok;
+        if (p.wpk) {
+          // stage k0 / 64, row block (n0 + 8 blk) / 16, rows (8 blk) % 16 .. +7: 1 KiB contiguous
+          o = (uint32_t)((((k0 >> 6) * nbw + ((n0 >> 4) + (blk >> 1))) * 16 + (blk & 1) * 8) * 128) + lpk[par];
+          okw = ok && n0 + blk * 8 < p.N;
+        } else {
+          o = (uint32_t)(blk * 8 * p.ldw * 2) + lw[par] + (uint32_t)k0 * 2u;
+        }
+        dma16_nt(rsW, wring + (st % S::WD) * WST + blk * 1024, okw ? o : kOOB);
       } else {
         const uint32_t o = (uint32_t)(blk * 8 * p.ldx * 2) + lx[par] + (uint32_t)k0 * 2u;
         dma16(rsX, xring + (st & 1) * XST + blk * 1024, ok ? o : kOOB);

@@ -96,6 +96,8 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
   const int tiles_m = p.tiles_m;
   const int64_t ldw = p.ldw, ldx = p.ldx;
   const uint16_t* const Wp = p.W;
+  const bool wpk = p.wpk != 0;  // W in the packed layout
+  const int nbw = N >> 4;       // its 16-row blocks
   const uint16_t* const Xp = p.X;
 
   // XCD-aware logical id: the hardware sends workgroup b to XCD b mod 8; consecutive logical ids share an XCD.
@@ -153,9 +155,13 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     const int n0 = (tau / tiles_m) * BN, m0 = (tau % tiles_m) * BM;
     const int kb = i0 * BK, ke = min(K, i1 * BK);
     const int nk = i1 - i0;
-    // descriptors cover this tile's rows only: rows past N (or M) read zeros
-    const __amdgpu_buffer_rsrc_t rsW = make_rsrc(Wp + (int64_t)n0 * ldw, (int64_t)min(BN, N - n0) * ldw * 2);
+    // descriptors cover this tile's rows only: rows past N (or M) read zeros. A packed W (stage-major
+    // [K/64][N/16][16][64], see ojx_pack_weight) is addressed through one descriptor over the whole buffer: W block
+    // blk of a stage is 1 KiB at row block n0/16 + blk/2, half blk & 1, and blocks past N are skipped.
+    const __amdgpu_buffer_rsrc_t rsW = wpk ? make_rsrc(Wp, (int64_t)N * K * 2)
+                                           : make_rsrc(Wp + (int64_t)n0 * ldw, (int64_t)min(BN, N - n0) * ldw * 2);
     const __amdgpu_buffer_rsrc_t rsX = make_rsrc(Xp + (int64_t)m0 * ldx, (int64_t)min(BM, M - m0) * ldx * 2);
+    const uint32_t dWp0 = (uint32_t)((((n0 >> 4) + (wave >> 1)) * 16 + (wave & 1) * 8 + (lane >> 3)) * 128 + kcol * 2);
 
 #pragma unroll
     for (int i = 0; i < FN; ++i)
@@ -173,7 +179,11 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       const uint32_t o_ = i < GW ? dW0 + i * stepW : real_ ? dX0 + (i - GW) * stepX : dXl;                 \
       const bool ok_ = (k0) + (real_ ? kcol : kcoll) < ke;                                                 \
       const int blk_ = real_ ? wave + i * NW : NBLK - 1;                                                   \
-      if (i < GW) dma16_nt(rsW, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);               \
+      if (i < GW) {                                                                                        \
+        const uint32_t op_ = dWp0 + i * (NW / 2 * 2048) + (uint32_t)((k0) >> 6) * nbw * 2048u;             \
+        const bool okw_ = ok_ && (!wpk || n0 + blk_ * 8 < N);                                               \
+        dma16_nt(rsW, smem + (buf) * STAGE + blk_ * 1024, okw_ ? (wpk ? op_ : o_ + kof_) : kOOB);          \
+      }                                                                                                    \
       else dma16(rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);                         \
     }                                                                                                      \
   } while (0)

@@ -77,6 +77,7 @@ struct GemmParams {
   // persistent stream-K kernels (family 5) only
   float* sk_ws;                     // partial-tile slots, 2 per workgroup, BN*BM fp32 each
   int dp_tiles;                     // tiles done whole first (a multiple of the grid)
+  int wpk;                          // 1: W is in the stage-major packed layout (family 6 only; see ojx_pack_weight)
   int sk_grid;                      // workgroups that share the remaining tiles' K iterations
 };
 
@@ -115,5 +116,8 @@ hipError_t launch_head_gemv(const uint16_t* hn, int64_t rows, const int64_t* las
                             const float* bias, float* scores, int H, hipStream_t st);
 hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* packed, int I, int K,
                                hipStream_t st);
+// W [N, K] row-major -> packed [K/64][N/16][16][64]: the 16-row x 64-k blocks of one 64-k stage of all rows are
+// contiguous, so a tile's weights for one stage are one contiguous run (N % 16 == 0, K % 64 == 0).
+hipError_t launch_pack_weight(const uint16_t* w, uint16_t* wp, int64_t N, int64_t K, hipStream_t st);
 
 }  // namespace ojx

@@ -152,7 +152,9 @@ def act_tables(like):
 
 # ------------------------------------------------------------------------------------------------ projections
 def mm(x, w, cfg=None):
-    """y = x . w^T, bf16 out (the reference's _mm / lt_matmul / F.linear)."""
+    """y = x . w^T, bf16 out (the reference's _mm / lt_matmul / F.linear). w may be a packed weight (pack_weight)."""
+    if w.dim() == 4:
+        return mm_pk(x, w, cfg)
     _chk(x, "x", torch.bfloat16)
     _chk(w, "w", torch.bfloat16)
     M, K = x.shape
@@ -179,7 +181,10 @@ def mm_splitk_f32(x, w, S, tile=-1):
 
 
 def mm_silu_mul(x, w_gu_packed, cfg=None):
-    """out [M, I] = bf16(bf16(silu(g)) * u), [g | u] = x . W_gu^T, W_gu in pack_gate_up layout [2I, K]."""
+    """out [M, I] = bf16(bf16(silu(g)) * u), [g | u] = x . W_gu^T, W_gu in pack_gate_up layout [2I, K] (or that
+    weight through pack_weight)."""
+    if w_gu_packed.dim() == 4:
+        return mm_silu_mul_pk(x, w_gu_packed, cfg)
     _chk(x, "x", torch.bfloat16)
     _chk(w_gu_packed, "w_gu", torch.bfloat16)
     M, K = x.shape
@@ -194,7 +199,10 @@ def mm_silu_mul(x, w_gu_packed, cfg=None):
 
 
 def mm_residual_rmsnorm(h, y, w, w1, rowmask, eps, want_hn=True, cfg=None):
-    """(h_new, hn): h_new = bf16(h + bf16(y . w^T)); hn = RMSNorm(h_new) * w1 (zero where rowmask == 0)."""
+    """(h_new, hn): h_new = bf16(h + bf16(y . w^T)); hn = RMSNorm(h_new) * w1 (zero where rowmask == 0). w may be a
+    packed weight (pack_weight)."""
+    if w.dim() == 4:
+        return mm_residual_rmsnorm_pk(h, y, w, w1, rowmask, eps, want_hn, cfg)
     _chk(h, "h", torch.bfloat16)
     _chk(y, "y", torch.bfloat16)
     _chk(w, "w", torch.bfloat16)
@@ -244,3 +252,71 @@ def pack_gate_up(gate, up):
     packed = torch.empty((2 * I, K), dtype=gate.dtype, device=gate.device)
     check(lib().ojx_pack_gate_up(_ptr(gate), _ptr(up), _ptr(packed), I, K, _stream()))
     return packed
+
+
+# ------------------------------------------------------------------------------------------------ packed weights
+def pack_weight(w):
+    """The load-time weight layout of the *_pk projections: W [N, K] -> [K/64, N/16, 16, 64] (ojx_pack_weight). For
+    the fused gate-up, pack pack_gate_up's output."""
+    _chk(w, "w", torch.bfloat16)
+    N, K = w.shape
+    if N % 16 or K % 64:
+        raise RuntimeError(f"pack_weight needs N % 16 == 0 and K % 64 == 0, got {tuple(w.shape)}")
+    wp = torch.empty((K // 64, N // 16, 16, 64), dtype=w.dtype, device=w.device)
+    check(lib().ojx_pack_weight(_ptr(w), _ptr(wp), N, K, _stream()))
+    return wp
+
+
+def _pk_shape(wp):
+    _chk(wp, "wp", torch.bfloat16)
+    if wp.dim() != 4 or tuple(wp.shape[2:]) != (16, 64):
+        raise RuntimeError(f"a packed weight is [K/64, N/16, 16, 64], got {tuple(wp.shape)}")
+    return wp.shape[1] * 16, wp.shape[0] * 64
+
+
+def mm_pk(x, wp, cfg=None):
+    """mm with a packed weight (pack_weight)."""
+    _chk(x, "x", torch.bfloat16)
+    N, K = _pk_shape(wp)
+    M = x.shape[0]
+    if x.shape[1] != K:
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)}, packed weight of K={K}")
+    y = torch.empty((M, N), dtype=x.dtype, device=x.device)
+    ws, nws = _workspace(M, N, K, KIND_PLAIN | _lib.KIND_PACKED, cfg, x.device)
+    check(lib().ojx_gemm_bf16_pk(_ptr(x), _ptr(wp), _ptr(y), M, N, K, K, N, _ptr(ws), nws, _cfgp(cfg), _stream()))
+    return y
+
+
+def mm_silu_mul_pk(x, wgu_pk, cfg=None):
+    """mm_silu_mul with the packed gate-up weight (pack_weight(pack_gate_up(gate, up)))."""
+    _chk(x, "x", torch.bfloat16)
+    N, K = _pk_shape(wgu_pk)
+    M = x.shape[0]
+    if x.shape[1] != K:
+        raise RuntimeError(f"shape mismatch: x {tuple(x.shape)}, packed weight of K={K}")
+    out = torch.empty((M, N // 2), dtype=x.dtype, device=x.device)
+    ws, nws = _workspace(M, N, K, KIND_SILU_MUL | _lib.KIND_PACKED, cfg, x.device)
+    check(lib().ojx_gemm_silu_mul_pk(_ptr(x), _ptr(wgu_pk), _ptr(out), M, N // 2, K, _ptr(ws), nws, _cfgp(cfg),
+                                     _stream()))
+    return out
+
+
+def mm_residual_rmsnorm_pk(h, y, wp, w1, rowmask, eps, want_hn=True, cfg=None):
+    """mm_residual_rmsnorm with a packed weight."""
+    _chk(h, "h", torch.bfloat16)
+    _chk(y, "y", torch.bfloat16)
+    N, K = _pk_shape(wp)
+    M = y.shape[0]
+    if y.shape[1] != K or tuple(h.shape) != (M, N):
+        raise RuntimeError(f"shape mismatch: h {tuple(h.shape)} y {tuple(y.shape)}, packed weight N={N} K={K}")
+    if want_hn:
+        _chk(w1, "w1", torch.float32)
+    if rowmask is not None:
+        _chk(rowmask, "rowmask", torch.int32)
+    h_new = torch.empty_like(h)
+    hn = torch.empty_like(h) if want_hn else None
+    ws, nws = _workspace(M, N, K, KIND_RESIDUAL | _lib.KIND_PACKED, cfg, y.device)
+    check(lib().ojx_gemm_residual_rmsnorm_pk(_ptr(y), _ptr(wp), _ptr(h), _ptr(w1) if want_hn else None,
+                                             _ptr(rowmask), float(eps), _ptr(h_new), _ptr(hn), M, N, K, _ptr(ws),
+                                             nws, _cfgp(cfg), _stream()))
+    return h_new, hn

@@ -37,10 +37,15 @@ def _split_forced():
     return any(os.environ.get(n) for n in _SPLIT_ENV)
 
 
+def _nk(w):
+    """(N, K) of a weight, row-major [N, K] or packed [K/64, N/16, 16, 64]."""
+    return (w.shape[1] * 16, w.shape[0] * 64) if w.dim() == 4 else (w.shape[0], w.shape[1])
+
+
 def _wsk_2d(wsk, what):
-    if wsk.dim() != 2:
-        raise RuntimeError(f"{what}: the split-K weight must be W itself, [N, K] (FastProjections._split returns it "
-                           f"unchanged); got shape {tuple(wsk.shape)}, the reference's [S, K/S, N] copy "
+    if wsk.dim() not in (2, 4):
+        raise RuntimeError(f"{what}: the split-K weight must be W itself, [N, K] or packed (FastProjections._split "
+                           f"returns it unchanged); got shape {tuple(wsk.shape)}, the reference's [S, K/S, N] copy "
                            "(src/fastmodel.py:186-188), which libojx does not read")
     return wsk
 
@@ -59,31 +64,41 @@ class FastProjections:
         return W
 
     @staticmethod
-    def merge_mlp(gate_w, up_w, down_w, keep_cat=False):
-        """d.w_gu / d.w_down of src/fastmodel.py:90-92. d.w_gu_packed is the fused gate-up layout ([2I, K]);
-        keep_cat also keeps the reference's cat[gate; up] for the unfused _silu_mul(_mm(hn, d.w_gu)) call."""
+    def _layout(W, pack):
+        """W itself, or with pack (the default) W in the stage-major packed layout (ext.pack_weight) when its shape
+        allows (N % 16 == 0, K % 64 == 0): one copy of every weight, in the layout the kernels stream fastest."""
+        W = W.contiguous()
+        if pack and W.shape[0] % 16 == 0 and W.shape[1] % 64 == 0:
+            return ext.pack_weight(W)
+        return W
+
+    @staticmethod
+    def merge_mlp(gate_w, up_w, down_w, keep_cat=False, pack=True):
+        """d.w_gu / d.w_down of src/fastmodel.py:90-92. d.w_gu_packed is the fused gate-up layout ([2I, K] rows,
+        packed by ext.pack_weight when pack); keep_cat also keeps the reference's cat[gate; up] (row-major) for the
+        unfused _silu_mul(_mm(hn, d.w_gu)) call."""
         d = SimpleNamespace()
-        d.w_gu_packed = ext.pack_gate_up(gate_w.contiguous(), up_w.contiguous())
+        d.w_gu_packed = FastProjections._layout(ext.pack_gate_up(gate_w.contiguous(), up_w.contiguous()), pack)
         d.w_gu = torch.cat([gate_w, up_w], 0).contiguous() if keep_cat else None
-        d.w_down = down_w.contiguous()
+        d.w_down = FastProjections._layout(down_w, pack)
         d.sk_down = _env_split("OJ_SK_DOWN")
         d.w_down_sk = d.w_down
         return d
 
     @staticmethod
-    def merge_linear_attn(d, qkv_w, z_w, b_w, a_w, out_w):
+    def merge_linear_attn(d, qkv_w, z_w, b_w, a_w, out_w, pack=True):
         """Linear-attention in/out projections (src/fastmodel.py:93-97): w_in = cat[qkv, z, b, a]."""
-        d.w_in = torch.cat([qkv_w, z_w, b_w, a_w], 0).contiguous()
-        d.w_out = out_w.contiguous()
+        d.w_in = FastProjections._layout(torch.cat([qkv_w, z_w, b_w, a_w], 0), pack)
+        d.w_out = FastProjections._layout(out_w, pack)
         d.sk_out = _env_split("OJ_SK_LIN_OUT")
         d.w_out_sk = d.w_out
         return d
 
     @staticmethod
-    def merge_full_attn(d, q_w, k_w, v_w, o_w):
+    def merge_full_attn(d, q_w, k_w, v_w, o_w, pack=True):
         """Full-attention in/out projections (src/fastmodel.py:104-109): w_in = cat[q, k, v]."""
-        d.w_in = torch.cat([q_w, k_w, v_w], 0).contiguous()
-        d.w_out = o_w.contiguous()
+        d.w_in = FastProjections._layout(torch.cat([q_w, k_w, v_w], 0), pack)
+        d.w_out = FastProjections._layout(o_w, pack)
         d.sk_out = _env_split("OJ_SK_FULL_OUT")
         d.w_out_sk = d.w_out
         return d
@@ -91,16 +106,18 @@ class FastProjections:
     # ------------------------------------------------------------------------------------- tuning (table)
     def _tune(self, x, w):
         M, K = x.shape
-        N = w.shape[0]
-        c = _lib.plan(M, N, K, _lib.KIND_PLAIN)
-        self._lt_best[(M, N, K)] = c
+        N, _ = _nk(w)
+        c = _lib.plan(M, N, K, _lib.KIND_PLAIN | (_lib.KIND_PACKED if w.dim() == 4 else 0))
+        self._lt_best[(M, N, K, w.dim())] = c
         return c
 
     def _tune_sk(self, y, wsk, S):
         """Tile for the split-K partial GEMM (_skmm): the residual plan's tile when it writes split-K planes, else -1
         (the library then picks a plane-writing tile itself; the persistent family has no K planes)."""
         M, K = y.shape
-        N = _wsk_2d(wsk, "_tune_sk").shape[0]
+        if _wsk_2d(wsk, "_tune_sk").dim() == 4:
+            raise RuntimeError("_skmm / _tune_sk: the split-K plane GEMM takes a row-major W [N, K]")
+        N = wsk.shape[0]
         c = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
         tile = c.tile if _lib.tile_info(c.tile)["family"] != 5 else -1
         self._sk_best[(M, N, K, S)] = tile
@@ -108,7 +125,7 @@ class FastProjections:
 
     # ------------------------------------------------------------------------------------- projections
     def _mm(self, x, w):
-        key = (x.shape[0], w.shape[0], x.shape[1])
+        key = (x.shape[0], _nk(w)[0], x.shape[1], w.dim())
         c = self._lt_best.get(key)
         if c is None:
             c = self._tune(x, w)
@@ -140,18 +157,19 @@ class FastProjections:
         an OJ_SK_* variable is set, as a split-K count with a tile that writes K planes."""
         W = w if w is not None else _wsk_2d(wsk, "_res")
         M, K = y.shape
-        N = W.shape[0]
+        N, _ = _nk(W)
         cfg = None
         if S and _split_forced():
-            cfg = self._forced_cfg(M, N, K, int(S))
+            cfg = self._forced_cfg(M, N, K, int(S), W.dim() == 4)
         return ext.mm_residual_rmsnorm(h, y, W, w1, mask, self.eps, want_hn=True, cfg=cfg)
 
     @staticmethod
-    def _forced_cfg(M, N, K, S):
+    def _forced_cfg(M, N, K, S, packed=False):
         """(tile, S) for an explicit split-K count: the plan's tile if it writes K planes, else the first candidate
         with that split that does. None (the plan) if no candidate takes S for this shape."""
-        plan = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
-        cands = [c for c in _lib.candidates(M, N, K, _lib.KIND_RESIDUAL)
+        kind = _lib.KIND_RESIDUAL | (_lib.KIND_PACKED if packed else 0)
+        plan = _lib.plan(M, N, K, kind)
+        cands = [c for c in _lib.candidates(M, N, K, kind)
                  if c.splitk == S and _lib.tile_info(c.tile)["family"] != 5]
         for c in cands:
             if c.tile == plan.tile:

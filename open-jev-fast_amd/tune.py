@@ -51,6 +51,8 @@ def main():
                     "many per CU")
     ap.add_argument("--no-tails", action="store_true", help="simple (tile, split-K) candidates only")
     ap.add_argument("--sk-splits", default="1,2,3,4,6,8", help="stream-K spreads tried for the persistent family")
+    ap.add_argument("--packed", action="store_true", help="tune the packed-weight entry points (kind | 4; the "
+                    "weights go through ojx_pack_weight, the K-interleaved family runs them)")
     args = ap.parse_args()
     Ms = [int(m) for m in args.m.split(",")] if args.m else list(M_DEFAULT)
     sk_splits = {int(v) for v in args.sk_splits.split(",")}
@@ -59,19 +61,23 @@ def main():
     dev = "cuda"
     for name in names:
         N, K, kind = TUNE_SHAPES[name]
-        kid = KIND_ID[kind]
-        ws = [(torch.randn(N, K, device=dev) * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+        kid = KIND_ID[kind] | (_lib.KIND_PACKED if args.packed else 0)
+        ws_rm = [(torch.randn(N, K, device=dev) * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+        ws = [ext.pack_weight(w) for w in ws_rm] if args.packed else ws_rm
         for M in Ms:
             x = torch.randn(M, K, device=dev).bfloat16()
             res = torch.randn(M, N, device=dev).bfloat16() if kind == "residual" else None
             w1 = torch.ones(N, device=dev)
 
+            mm, mm_silu, mm_res = ((ext.mm_pk, ext.mm_silu_mul_pk, ext.mm_residual_rmsnorm_pk) if args.packed else
+                                   (ext.mm, ext.mm_silu_mul, ext.mm_residual_rmsnorm))
+
             def call(w, c):
                 if kind == "plain":
-                    return lambda: ext.mm(x, w, cfg=c)
+                    return lambda: mm(x, w, cfg=c)
                 if kind == "silu":
-                    return lambda: ext.mm_silu_mul(x, w, cfg=c)
-                return lambda: ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6, cfg=c)
+                    return lambda: mm_silu(x, w, cfg=c)
+                return lambda: mm_res(res, x, w, w1, None, 1e-6, cfg=c)
 
             results = []
             only = {int(t) for t in args.tiles.split(",")} if args.tiles else None
@@ -97,7 +103,7 @@ def main():
                     if wgs > args.max_waves * 256:
                         continue
                 timed((c.tile, c.splitk, 0, 1, 0))
-            if kind != "residual" and not args.no_tails:
+            if kind != "residual" and not args.no_tails and not args.packed:
                 # tail configurations: the best simple tiles over whole rounds of 256 workgroups, the leftover
                 # rows with a finer tile
                 simple = sorted(results)
@@ -131,18 +137,19 @@ def main():
             for t, key in results[:5]:
                 cc = _lib.cfg(*key)
                 w = ws[0]
+                wr = ws_rm[0]
                 if kind == "plain":
-                    out = ext.mm(x, w, cfg=cc).float()
-                    ref = (x.float() @ w.float().t()).bfloat16().float()
+                    out = mm(x, w, cfg=cc).float()
+                    ref = (x.float() @ wr.float().t()).bfloat16().float()
                 elif kind == "silu":
-                    out = ext.mm_silu_mul(x, w, cfg=cc).float()
-                    gu = (x.float() @ w.float().t()).view(M, N // 8, 2, 4)
+                    out = mm_silu(x, w, cfg=cc).float()
+                    gu = (x.float() @ wr.float().t()).view(M, N // 8, 2, 4)
                     g, u = gu[:, :, 0].reshape(M, N // 2), gu[:, :, 1].reshape(M, N // 2)
                     g, u = g.bfloat16().float(), u.bfloat16().float()
                     ref = ((g / (1 + torch.exp(-g))).bfloat16().float() * u).bfloat16().float()
                 else:
-                    out = ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6, want_hn=False, cfg=cc)[0].float()
-                    ref = (res.float() + (x.float() @ w.float().t()).bfloat16().float()).bfloat16().float()
+                    out = mm_res(res, x, w, w1, None, 1e-6, want_hn=False, cfg=cc)[0].float()
+                    ref = (res.float() + (x.float() @ wr.float().t()).bfloat16().float()).bfloat16().float()
                 d = (out - ref).abs()
                 ok = (d.max() / ref.abs().max() <= 1e-2) and (d.mean() <= 1e-3 * ref.pow(2).mean().sqrt())
                 if bool(ok):
@@ -161,7 +168,7 @@ def main():
                               "frac": round(r["frac"], 4), "tflops": round(r["tflops"], 1),
                               "gbs": round(r["gbs"], 1), "top": top}), flush=True)
             rows.append((M, N, K, kid, key, t))
-        del ws
+        del ws, ws_rm
         torch.cuda.empty_cache()
     if args.out:
         with open(args.out, "w") as f:

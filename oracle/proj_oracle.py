@@ -16,6 +16,7 @@ What it restates (reference file:line):
   gate_up_silu       _silu_mul(_mm(hn, cat[gate; up])) (src/fastmodel.py:90, 478, 190-194)
   pack_gate_up       the fused-GEMM weight layout (rows in blocks of 8: 4 gate rows, 4 up rows) — libojx's own
                      layout, restated here so tests can build it on the CPU
+  pack_weight        the stage-major packed weight layout of the *_pk projections (libojx's own), likewise
   linear_f64         fp64 brute-force dot products (numpy), the independent check the oracle is pinned against
   head_scores        mdl.head(hn[lastidx].float()).squeeze(-1) (src/server.py:37, 57, 129; hn[lastidx] at
                      src/fastmodel.py:314, 482) for a Linear(H, 1) with fp32 weight and bias: torch fp32 on the CPU.
@@ -118,6 +119,13 @@ def pack_gate_up(gate, up):
     """[2I, K]: rows in blocks of 8 = gate rows 4b..4b+3 then up rows 4b..4b+3."""
     I, K = gate.shape
     return torch.stack([gate.view(I // 4, 4, K), up.view(I // 4, 4, K)], 1).reshape(2 * I, K)
+
+
+def pack_weight(w):
+    """The packed weight layout of libojx's *_pk projections, restated: W [N, K] -> [K/64, N/16, 16, 64] with
+    packed[s, b, r, c] = W[16 b + r, 64 s + c] (libojx's own layout, so that tests can build it on the CPU)."""
+    N, K = w.shape
+    return w.reshape(N // 16, 16, K // 64, 64).permute(2, 0, 1, 3).contiguous()
 
 
 def head_scores(hn, lastidx, w, bias=None):

@@ -81,24 +81,31 @@ def test_unpack_inverts_pack(O):
 # --------------------------------------------------------------------------------------- every plan-table row
 @pytest.mark.parametrize("M,N,K,kind", plan_rows(), ids=lambda v: str(v))
 def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
+    """Rows of kind | 4 are plans for packed weights: the call goes through the *_pk entry point."""
     plan = pkg._lib.plan(M, N, K, kind)
     _say(f"case plan row M={M} N={N} K={K} kind={kind} plan={plan}")
+    packed = bool(kind & 4)
+    kind &= 3
+    mm = ext.mm_pk if packed else ext.mm
+    mm_silu = ext.mm_silu_mul_pk if packed else ext.mm_silu_mul
+    mm_res = ext.mm_residual_rmsnorm_pk if packed else ext.mm_residual_rmsnorm
     gen = torch.Generator().manual_seed(M * 31 + N + K)
     gx = torch.Generator(device=dev).manual_seed(M + N)
     x = torch.randn(M, K, generator=gx, device=dev).bfloat16()
     w = weight(N, K, dev)
+    wk = ext.pack_weight(w) if packed else w
     mrows = sample_idx(M, 24, gen, extra=(15, 16, 31, 32, 95, 96, 143, 144, 191, 192, 255, 256, 287, 288))
     xs = x[mrows.to(dev)].cpu()
     ref_cfg = pkg._lib.cfg(0, 1)
     if kind == 0:
-        y = ext.mm(x, w)
+        y = mm(x, wk)
         cols = sample_idx(N, 384, gen, extra=(N - plan.tail_rows - 1, N - plan.tail_rows) if plan.tail_rows else ())
         ref = O.linear_bf16(xs, w[cols.to(dev)].cpu())
         _assert_tol(O, y[mrows.to(dev)][:, cols.to(dev)], ref, "sampled vs oracle")
         _assert_tol(O, y, ext.mm(x, w, cfg=ref_cfg), "every element vs the family-0 tile")
     elif kind == 1:
         I = N // 2
-        out = ext.mm_silu_mul(x, w)
+        out = mm_silu(x, wk)
         tail_col = (N - plan.tail_rows) // 2
         cols = sample_idx(I, 384, gen, extra=(tail_col - 1, tail_col) if plan.tail_rows else ())
         gate, up = unpack_gate_up(w)
@@ -109,7 +116,7 @@ def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
         res = torch.randn(M, N, generator=gx, device=dev).bfloat16()
         w1 = (1.0 + 0.1 * torch.randn(N, generator=gx, device=dev)).float()
         mask = (torch.rand(M, generator=gx, device=dev) > 0.2).int()
-        h, hn = ext.mm_residual_rmsnorm(res, x, w, w1, mask, 1e-6)
+        h, hn = mm_res(res, x, wk, w1, mask, 1e-6)
         rh, rhn = O.residual_proj(res[mrows.to(dev)].cpu(), xs, w.cpu(), w1.cpu(), mask[mrows.to(dev)].cpu(), 1e-6)
         _assert_tol(O, h[mrows.to(dev)], rh, "h sampled rows vs oracle")
         _assert_tol(O, hn[mrows.to(dev)], rhn, "hn sampled rows vs oracle")
@@ -251,8 +258,9 @@ def test_fastprojections_reference_call_pattern(pkg, ext, O, dev, monkeypatch):
     m_fused = P._mm_silu(hn1, d.w_gu_packed)
     # the two paths may run tile families with different K summation orders: equal to rounding, both vs the oracle
     _assert_tol(O, m_fused, m, "fused gate-up vs GEMM -> silu_mul_lut")
+    assert d.w_down.dim() == 4 and d.w_gu_packed.dim() == 4, "merge_mlp packs the weights by default"
     h2, hn2 = P._res(h1, m, d.w_down_sk, d.sk_down, w1, mask, w=d.w_down)
-    e2 = ext.mm_residual_rmsnorm(h1, m, w_down, w1, mask, 1e-6)
+    e2 = ext.mm_residual_rmsnorm(h1, m, d.w_down, w1, mask, 1e-6)
     assert torch.equal(h2, e2[0]) and torch.equal(hn2, e2[1])
 
     rows = sample_idx(M, 8, torch.Generator().manual_seed(1)).to(dev)
@@ -270,10 +278,10 @@ def test_fastprojections_reference_call_pattern(pkg, ext, O, dev, monkeypatch):
 
     _say("case shim layer, OJ_SK_DOWN=2")
     monkeypatch.setenv("OJ_SK_DOWN", "2")
-    f2 = fp.FastProjections._forced_cfg(M, H, I, 2)
+    f2 = fp.FastProjections._forced_cfg(M, H, I, 2, packed=True)
     assert f2 is not None and f2.splitk == 2 and pkg._lib.tile_info(f2.tile)["family"] != 5
     h3, hn3 = P._res(h1, m, d.w_down_sk, d.sk_down, w1, mask, w=d.w_down)
-    e3 = ext.mm_residual_rmsnorm(h1, m, w_down, w1, mask, 1e-6, cfg=f2)
+    e3 = ext.mm_residual_rmsnorm(h1, m, d.w_down, w1, mask, 1e-6, cfg=f2)
     assert torch.equal(h3, e3[0]) and torch.equal(hn3, e3[1]), "OJ_SK_DOWN=2 not applied"
     _assert_tol(O, c(h3), rh2, "_res down h (split 2)")
     _assert_tol(O, c(hn3), rhn2, "_res down hn (split 2)")

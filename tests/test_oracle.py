@@ -231,3 +231,17 @@ def test_head_scores_oracle_pinned(O):
         assert torch.equal(O.head_scores(hn, idx, e), hn[idx, j].float())
     perm = torch.randperm(R, generator=g)
     assert torch.allclose(O.head_scores(hn, idx[perm], w, b), s[perm], rtol=1e-6, atol=1e-6)
+
+
+def test_pack_weight_layout_bruteforce():
+    """The packed layout against its definition, element by element, on bit patterns that identify every element."""
+    N, K = 32, 128
+    bits = torch.arange(N * K, dtype=torch.int32).to(torch.int16).view(N, K)
+    w = bits.view(torch.bfloat16)
+    p = O.pack_weight(w).view(torch.int16)
+    assert tuple(p.shape) == (K // 64, N // 16, 16, 64)
+    for s in range(K // 64):
+        for b in range(N // 16):
+            for r in range(16):
+                for c in range(64):
+                    assert int(p[s, b, r, c]) == int(bits[16 * b + r, 64 * s + c])
