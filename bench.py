@@ -37,9 +37,16 @@ def load():
     return pkg, import_module("open_jev_fast_amd.ext"), import_module("open_jev_fast_amd.perf")
 
 
+PACKED = True   # weights in the library's load-time packed layout (ext.pack_weight); --rowmajor turns it off
+
+
 def make_weights(N, K, copies, std=0.02, seed=0, dev="cuda"):
+    """Seeded weights [N, K], in the packed layout when PACKED (the layout FastProjections loads weights in)."""
+    from importlib import import_module
+    ext = import_module("open_jev_fast_amd.ext")
     g = torch.Generator(device=dev).manual_seed(seed)
-    return [(torch.randn(N, K, generator=g, device=dev) * std).bfloat16() for _ in range(copies)]
+    ws = [(torch.randn(N, K, generator=g, device=dev) * std).bfloat16() for _ in range(copies)]
+    return [ext.pack_weight(w) for w in ws] if PACKED else ws
 
 
 def shape_call(ext, kind, x, w, res=None, w1=None):
@@ -112,7 +119,7 @@ def main_default(args, pkg, ext, perf):
     g = torch.Generator(device=dev).manual_seed(1)
     x = torch.randn(M, K, generator=g, device=dev).bfloat16()
     ws = make_weights(N, K, 2, seed=2)
-    plan = pkg._lib.plan(M, N, K, pkg._lib.KIND_SILU_MUL)
+    plan = pkg._lib.plan(M, N, K, pkg._lib.KIND_SILU_MUL | (pkg._lib.KIND_PACKED if PACKED else 0))
     fns = [lambda w=w: ext.mm_silu_mul(x, w) for w in ws]
 
     # warm-up (untimed), then one graph of exactly K steps
@@ -161,10 +168,12 @@ def main_default(args, pkg, ext, perf):
     n1 = N - plan.tail_rows
     fam = pkg._lib.tile_info(plan.tile)["family"]
     if plan.splitk > 1 and fam != 5:
+        if PACKED:
+            raise RuntimeError("the dominant-kernel timing of a split-K packed plan is not implemented")
         dom = [lambda w=w: ext.mm_splitk_f32(x, w[:n1], plan.splitk, tile=plan.tile) for w in ws]
         dom_name = "gemm (split-K partial pass)"
     else:
-        dom = [lambda w=w: ext.mm_silu_mul(x, w[:n1], cfg=(plan.tile, plan.splitk)) for w in ws]
+        dom = [lambda w=w: ext.mm_silu_mul(x, w if PACKED else w[:n1], cfg=(plan.tile, plan.splitk)) for w in ws]
         dom_name = ("persistent stream-K gemm (fused SiLU.mul epilogue) + split-tile fixup, one call of two "
                     "launches" if fam == 5 else "gemm (fused SiLU.mul epilogue)")
     dom_name += f", W rows 0..{n1} of {N}" if plan.tail_rows else ""
@@ -185,7 +194,7 @@ def main_default(args, pkg, ext, perf):
         achieved, peak, unit = kbytes / k_s / 1e9, perf.HBM_PEAK / 1e9, "GB/s"
     else:
         achieved, peak, unit = kflops / k_s / 1e12, perf.MFMA_BF16_PEAK / 1e12, "TFLOP/s"
-    tkey = f"gate_up_silu_M{M}_tile{plan.tile}_s{plan.splitk}_rows{n1}"
+    tkey = f"gate_up_silu_M{M}_tile{plan.tile}_s{plan.splitk}_rows{n1}" + ("_packed" if PACKED else "")
     roof = {"bound": bound, "achieved": round(achieved, 1), "peak": peak, "unit": unit,
             "frac": round(achieved / peak, 4), "traffic": traffic_from_profiles(tkey),
             "kernel": dom_name, "kernel_us": round(k_s * 1e6, 2), "algorithmic_bytes": kbytes,
@@ -203,9 +212,11 @@ def main_default(args, pkg, ext, perf):
         "metric": METRIC, "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms, 5), "replays_ms": [round(v, 4) for v in reps], "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
-        "data": "synthetic: seeded x ~ N(0,1), W ~ N(0,0.02^2), bf16; 2 rotating weight copies",
+        "data": "synthetic: seeded x ~ N(0,1), W ~ N(0,0.02^2), bf16; 2 rotating weight copies"
+                + ("; weights in the load-time packed layout (ojx_pack_weight)" if PACKED else "; row-major weights"),
         "config": {"workload": "gate_up_silu: BASELINE configs[1], fused gate-up + SiLU.mul, M=288 K=5120 "
                                "I=17408 (W_gu 34816x5120)", "M": M, "N": N, "K": K,
+                   "weight_layout": "packed" if PACKED else "row-major",
                    "plan": {"tile": plan.tile, "splitk": plan.splitk, **pkg._lib.tile_info(plan.tile),
                             **({"tail_rows": plan.tail_rows, "tail_tile": plan.tail_tile,
                                 "tail_splitk": plan.tail_splitk} if plan.tail_rows else {})}},
@@ -235,7 +246,7 @@ def main_sweep(args, pkg, ext, perf):
         for m in Ms:
             rr = measure_shape(ext, perf, name, m)
             N, K, kind = perf.SHAPES[name]
-            c = pkg._lib.plan(m, N, K, {"plain": 0, "silu": 1, "residual": 2}[kind])
+            c = pkg._lib.plan(m, N, K, {"plain": 0, "silu": 1, "residual": 2}[kind] | (4 if PACKED else 0))
             print(json.dumps({"shape": name, "M": m, "N": N, "K": K, "tile": c.tile, "splitk": c.splitk,
                               **{k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}}), flush=True)
 
@@ -259,6 +270,8 @@ def main_stack(args, pkg, ext, perf):
             w_out=(torch.randn(H, full_out_k if full else lin_out_k, generator=g, device=dev) * std).bfloat16(),
             w_gu=(torch.randn(2 * I, H, generator=g, device=dev) * std).bfloat16(),
             w_dn=(torch.randn(H, I, generator=g, device=dev) * std).bfloat16()))
+        if PACKED:
+            layers[-1] = {k: ext.pack_weight(v) for k, v in layers[-1].items()}
     h0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
     hn0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
     y_att = torch.randn(M, lin_out_k, generator=g, device=dev).bfloat16()
@@ -318,22 +331,23 @@ def main_vs_hipblaslt(args, pkg, ext, perf):
     for name in names:
         N, K, kind = perf.SHAPES[name]
         ws = [(torch.randn(N, K, device=dev) * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+        wo = [ext.pack_weight(w) for w in ws] if PACKED else ws   # the layout this build loads weights in
         for M in Ms:
             x = torch.randn(M, K, device=dev).bfloat16()
             res = torch.randn(M, N, device=dev).bfloat16()
             w1 = torch.ones(N, device=dev)
             blas = [lambda w=w: torch.nn.functional.linear(x, w) for w in ws]
             if kind == "plain":
-                ours = [lambda w=w: ext.mm(x, w) for w in ws]
+                ours = [lambda w=w: ext.mm(x, w) for w in wo]
             elif kind == "silu":
-                ours = [lambda w=w: ext.mm_silu_mul(x, w) for w in ws]
+                ours = [lambda w=w: ext.mm_silu_mul(x, w) for w in wo]
             else:
-                ours = [lambda w=w: ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6) for w in ws]
+                ours = [lambda w=w: ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6) for w in wo]
             t_b = min(perf.gpu_time(blas, iters=10, reps=3), perf.gpu_time(blas, iters=10, reps=3))
             t_o = min(perf.gpu_time(ours, iters=10, reps=3), perf.gpu_time(ours, iters=10, reps=3))
             print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "epilogue": kind, "ojx_us": round(t_o * 1e6, 1),
                               "hipblaslt_gemm_us": round(t_b * 1e6, 1), "ratio": round(t_b / t_o, 3)}), flush=True)
-        del ws
+        del ws, wo
         torch.cuda.empty_cache()
 
 
@@ -351,6 +365,7 @@ def main():
     ap.add_argument("--shapes", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--rowmajor", action="store_true", help="row-major weights instead of the packed layout")
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or ws != 1:
@@ -361,6 +376,8 @@ def main():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
     pkg, ext, perf = load()
+    global PACKED
+    PACKED = not args.rowmajor
     if args.sweep:
         main_sweep(args, pkg, ext, perf)
     elif args.stack:

@@ -3,6 +3,7 @@
     rocprofv3 --kernel-trace --stats -d /tmp/prof -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
     rocprofv3 --pmc FETCH_SIZE -d /tmp/pmc -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
     python3 open-jev-fast_amd/prof.py --copy-mb 512     # plain copy kernel, to calibrate FETCH_SIZE / WRITE_SIZE
+    (--packed: weights in the packed layout of ext.pack_weight, the layout bench.py uses by default)
 
 Shapes are those of open_jev_fast_amd.perf.SHAPES (plus any --n/--k override); weights rotate over copies larger
 than the Infinity Cache so each call streams its weights from HBM.
@@ -27,6 +28,7 @@ def main():
     ap.add_argument("--splitk", type=int, default=1)
     ap.add_argument("--calls", type=int, default=40)
     ap.add_argument("--copy-mb", type=int, default=0)
+    ap.add_argument("--packed", action="store_true", help="weights in the packed layout (ext.pack_weight)")
     args = ap.parse_args()
     if args.copy_mb:
         n = args.copy_mb << 20
@@ -48,6 +50,8 @@ def main():
     cfg = pkg._lib.cfg(args.tile, args.splitk) if args.tile >= 0 else None
     x = torch.randn(M, K, device="cuda").bfloat16()
     ws = [(torch.randn(N, K, device="cuda") * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+    if args.packed:
+        ws = [ext.pack_weight(w) for w in ws]
     res = torch.randn(M, N, device="cuda").bfloat16()
     w1 = torch.ones(N, device="cuda")
     for i in range(args.calls):
@@ -59,7 +63,7 @@ def main():
         else:
             ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6, cfg=cfg)
     torch.cuda.synchronize()
-    c = cfg or pkg._lib.plan(M, N, K, {"plain": 0, "silu": 1, "residual": 2}[kind])
+    c = cfg or pkg._lib.plan(M, N, K, {"plain": 0, "silu": 1, "residual": 2}[kind] | (4 if args.packed else 0))
     print(f"{args.shape} M={M} N={N} K={K} tile={c.tile} splitk={c.splitk} calls={args.calls}", flush=True)
 
 
