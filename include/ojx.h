@@ -138,6 +138,27 @@ int ojx_gemm_residual_rmsnorm_pk(const void* x, const void* wp, const void* resi
                                  int64_t K, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg,
                                  ojx_stream_t stream);
 
+/* Full-attention prep, the consumer of the full-attention layers' QKV in-projection: replaces fullattn_prep2
+ * (src/kernels.cu:302-360; called as K.fullattn_prep2(proj, qw1, kw1, cos, sin, 1, N, HQ, HKV, D, eps) by
+ * forward_gtree, src/fastmodel.py:462). proj [N, (2 HQ + 2 HKV) D] bf16 (per q head: D q dims then D gate dims; then
+ * the k heads, then the v heads). q and k heads: RMSNorm over the head (weight qw1 / kw1 fp32 [D], eps), then the
+ * rotate-half RoPE on the first RD dims with cos / sin bf16 [N, RD]; outputs qt [HQ, N, D], kt [HKV, N, D],
+ * vt [HKV, N, D] (v copied) and gate [N, HQ D] (copied), all bf16. D = 256; RD = 8 * a power of two, <= D. */
+int ojx_fullattn_prep(const void* proj, int64_t N, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
+                      const float* qw1, const float* kw1, const void* cosb, const void* sinb, void* qt, void* kt,
+                      void* vt, void* gate, ojx_stream_t stream);
+
+/* The QKV in-projection with the prep fused into its epilogue: x [M, K] . W^T with W [(2 HQ + 2 HKV) D, K]
+ * (row-major, or packed by ojx_pack_weight when w_packed != 0), then ojx_fullattn_prep's arithmetic on the bf16
+ * projection of each 256-row head block, written straight to qt, kt, vt and gate: the [M, (2 HQ + 2 HKV) D]
+ * projection never goes to memory and the prep launch disappears. Replaces _mm(hn, d.w_in) followed by
+ * fullattn_prep2 (src/fastmodel.py:412,462). D = 256, RD = 64. Results equal _mm + ojx_fullattn_prep up to the
+ * order in which a head's sum of squares is added (fp32). */
+int ojx_gemm_qkv_fullattn_prep(const void* x, const void* w, int32_t w_packed, const float* qw1, const float* kw1,
+                               const void* cosb, const void* sinb, void* qt, void* kt, void* vt, void* gate,
+                               int64_t M, int64_t K, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
+                               ojx_stream_t stream);
+
 /* Bytes of the static device scratch behind ojx_gemm_residual_rmsnorm_noalloc (one array per GPU). */
 #define OJX_NOALLOC_SCRATCH_BYTES (32LL << 20)
 

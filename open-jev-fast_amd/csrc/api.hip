@@ -210,9 +210,10 @@ int check_dims(int64_t M, int64_t N, int64_t K) {
 int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, int64_t ldw, void* out, int64_t ldo,
          const void* res, int64_t ldr, int64_t M, int64_t N, int64_t K, hipStream_t st, void* ws = nullptr,
          int64_t ws_off = 0, const float* w1 = nullptr, const int32_t* rowmask = nullptr, float eps = 0.f,
-         uint16_t* hn_out = nullptr, bool packed = false) {
+         uint16_t* hn_out = nullptr, bool packed = false, const ojx::FattnParams* fa = nullptr) {
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
   ojx::GemmParams p;
+  p.fa = fa != nullptr ? *fa : ojx::FattnParams{};
   p.W = static_cast<const uint16_t*>(w);
   p.ldw = ldw;
   p.X = static_cast<const uint16_t*>(x);
@@ -267,6 +268,14 @@ int check_ws(void* ws, int64_t ws_bytes, int64_t need) {
     return fail(OJX_ERR_WORKSPACE, "workspace of %lld bytes needed, %lld given", (long long)need,
                 (long long)(ws == nullptr ? 0 : ws_bytes));
   if (!aligned(ws, 16)) return fail(OJX_ERR_ARG, "workspace must be 16-byte aligned");
+  return OJX_OK;
+}
+
+int check_packed_shape_int(int64_t N, int64_t K) {
+  if (N % 16 != 0 || K % 64 != 0)
+    return fail(OJX_ERR_SHAPE, "packed weights need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
+                (long long)K);
+  if (N * K * 2 >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "packed weight larger than 2 GiB");
   return OJX_OK;
 }
 
@@ -547,13 +556,7 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
                                     workspace_bytes, cfg, stream, false);
 }
 
-static int check_packed_shape(int64_t N, int64_t K) {
-  if (N % 16 != 0 || K % 64 != 0)
-    return fail(OJX_ERR_SHAPE, "packed weights need N %% 16 == 0 and K %% 64 == 0 (N=%lld K=%lld)", (long long)N,
-                (long long)K);
-  if (N * K * 2 >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "packed weight larger than 2 GiB");
-  return OJX_OK;
-}
+static int check_packed_shape(int64_t N, int64_t K) { return check_packed_shape_int(N, K); }
 
 int ojx_pack_weight(const void* w, void* wp, int64_t N, int64_t K, ojx_stream_t stream) {
   OJX_TRY(check_dims(1, N, K));
@@ -583,6 +586,53 @@ int ojx_gemm_residual_rmsnorm_pk(const void* x, const void* wp, const void* resi
   OJX_TRY(check_packed_shape(N, K));
   return gemm_residual_rmsnorm_impl(x, wp, residual, w1, rowmask, eps, h_out, hn_out, M, N, K, workspace,
                                     workspace_bytes, cfg, stream, true);
+}
+
+static int check_fattn(int64_t N, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, const float* qw1,
+                       const float* kw1, const void* cosb, const void* sinb, const void* qt, const void* kt,
+                       const void* vt, const void* gate) {
+  if (D != 256) return fail(OJX_ERR_SHAPE, "full-attention prep supports head_dim 256 (D=%d)", D);
+  if (HQ < 1 || HKV < 1 || HQ > 4096 || HKV > 4096) return fail(OJX_ERR_SHAPE, "bad head counts HQ=%d HKV=%d", HQ, HKV);
+  if (RD < 8 || RD > D || RD % 8 != 0 || ((RD / 8) & (RD / 8 - 1)) != 0)
+    return fail(OJX_ERR_SHAPE, "rotary dims RD=%d must be 8 * a power of two, <= D", RD);
+  if (N < 0 || N >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "bad token count");
+  if (N == 0) return OJX_OK;  // nothing is read or written
+  const void* ptrs[] = {qw1, kw1, cosb, sinb, qt, kt, vt, gate};
+  for (const void* q : ptrs)
+    if (q == nullptr || !aligned(q, 16)) return fail(OJX_ERR_ARG, "prep operands must be non-null, 16-byte aligned");
+  return OJX_OK;
+}
+
+int ojx_fullattn_prep(const void* proj, int64_t N, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
+                      const float* qw1, const float* kw1, const void* cosb, const void* sinb, void* qt, void* kt,
+                      void* vt, void* gate, ojx_stream_t stream) {
+  OJX_TRY(check_fattn(N, HQ, HKV, D, RD, qw1, kw1, cosb, sinb, qt, kt, vt, gate));
+  if (N == 0) return OJX_OK;
+  if (proj == nullptr || !aligned(proj, 16)) return fail(OJX_ERR_ARG, "proj must be non-null, 16-byte aligned");
+  return hip_check(ojx::launch_fullattn_prep(static_cast<const uint16_t*>(proj), N, HQ, HKV, RD, eps, qw1, kw1,
+                                             static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb),
+                                             static_cast<uint16_t*>(qt), static_cast<uint16_t*>(kt),
+                                             static_cast<uint16_t*>(vt), static_cast<uint16_t*>(gate),
+                                             static_cast<hipStream_t>(stream)), "prep launch");
+}
+
+int ojx_gemm_qkv_fullattn_prep(const void* x, const void* w, int32_t w_packed, const float* qw1, const float* kw1,
+                               const void* cosb, const void* sinb, void* qt, void* kt, void* vt, void* gate,
+                               int64_t M, int64_t K, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
+                               ojx_stream_t stream) {
+  OJX_TRY(check_fattn(M, HQ, HKV, D, RD, qw1, kw1, cosb, sinb, qt, kt, vt, gate));
+  if (RD != 64) return fail(OJX_ERR_SHAPE, "the fused prep epilogue supports RD = 64 (RD=%d)", RD);
+  const int64_t N = (int64_t)(2 * HQ + 2 * HKV) * D;
+  OJX_TRY(check_dims(M, N, K));
+  if (M == 0) return OJX_OK;
+  OJX_TRY(check_operands(x, w, K, K, K));
+  if (w_packed) OJX_TRY(check_packed_shape_int(N, K));
+  ojx_cfg c{M <= 64 ? 89 : 88, 1, 0, 1, 0};  // 256-row tiles: one head block each, no split (the norm needs sums)
+  ojx::FattnParams fa{qw1, kw1, static_cast<const uint16_t*>(cosb), static_cast<const uint16_t*>(sinb),
+                      static_cast<uint16_t*>(qt), static_cast<uint16_t*>(kt), static_cast<uint16_t*>(vt),
+                      static_cast<uint16_t*>(gate), HQ, HKV, RD, eps};
+  return gemm(c, ojx::EPI_FATTN, x, K, w, K, nullptr, 0, nullptr, 0, M, N, K, static_cast<hipStream_t>(stream),
+              nullptr, 0, nullptr, nullptr, 0.f, nullptr, w_packed != 0, &fa);
 }
 
 int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* residual, const float* w1,

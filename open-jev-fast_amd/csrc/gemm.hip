@@ -917,6 +917,8 @@ static const TileEntry kTiles[] = {
     OJX_KX(9, 2, 0),                // 85 144 x 128
     OJX_KX(8, 2, 0),                // 86 128 x 128
     OJX_KX(8, 1, 0),                // 87 128 x 64
+    OJX_KX(16, 2, 0),               // 88 256 x 128: one 256-dim attention head per tile (prep epilogue)
+    OJX_KX(16, 1, 0),               // 89 256 x 64
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

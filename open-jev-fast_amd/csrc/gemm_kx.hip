@@ -47,6 +47,105 @@ struct KxShape {
   static_assert(LDS <= 160 * 1024, "LDS");
 };
 
+// Full-attention prep epilogue of the QKV in-projection (EPI_FATTN; 256-row tiles = one head block, FX x fragments
+// per SIMD group, no leftover fragments). After the pair reduction wave g (h = 0) holds dims 0..127 and wave g+4
+// (h = 1) dims 128..255 of the group's 16 FX rows. The 256-row block n0 / 256 is a q head (even blocks below
+// 2 HQ), the gate of that head (odd blocks), a k head, or a v head. q and k: proj = bf16(acc), RMSNorm over the
+// head's 256 dims (each wave sums its half over its lanes, the pair adds through LDS), weight qw1 / kw1, then the
+// rotate-half RoPE on the first RD = 64 dims (the partner of dim d is in fragment d/16 +- 2 of the same lane),
+// stored head-major; gate and v: proj stored as it is. Same arithmetic as fullattn_prep_k (prep.hip), the
+// reference's fullattn_prep2_k (src/kernels.cu:302-355), except the order in which the sum of squares is added.
+template <int FW, int FX>
+__device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&acc)[FW][FX], int g, int h, int lane,
+                                                  int m0, int n0, uint8_t* smem) {
+  static_assert(FW == 16, "one 256-dim head per tile");
+  constexpr int D = 256, RDF = 2;  // RoPE dims = 64 = 4 fragments; partner fragment distance 2
+  const FattnParams& fa = p.fa;
+  const int lr = lane & 15, lg = lane >> 4;
+  const int cb = n0 / D;
+  const int type = cb < 2 * fa.HQ ? (cb & 1) : (cb < 2 * fa.HQ + fa.HKV ? 2 : 3);  // 0 q, 1 gate, 2 k, 3 v
+  const int hh = cb < 2 * fa.HQ ? cb >> 1 : (type == 2 ? cb - 2 * fa.HQ : cb - 2 * fa.HQ - fa.HKV);
+  const int M = p.M;
+  const int p0 = h * 8;  // this wave's fragments (positions = W fragments) p0 .. p0+7
+  if (type == 1 || type == 3) {
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp)
+#pragma unroll
+      for (int xi = 0; xi < FX; ++xi) {
+        const int m = m0 + (g * FX + xi) * 16 + lr;
+        if (m >= M) continue;
+        const f32x4 v = acc[p0 + pp][xi];
+        const uint2 o = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+        const int d = (p0 + pp) * 16 + lg * 4;
+        uint16_t* dst = type == 1 ? fa.gate + (int64_t)m * (fa.HQ * D) + hh * D + d
+                                  : fa.vt + ((int64_t)hh * M + m) * D + d;
+        *reinterpret_cast<uint2*>(dst) = o;
+      }
+    return;
+  }
+  // q or k: bf16 proj values, the head's sum of squares per row
+  float ss[FX];
+#pragma unroll
+  for (int xi = 0; xi < FX; ++xi) {
+    float s = 0.f;
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float x = rbf(acc[p0 + pp][xi][e]);
+        acc[p0 + pp][xi][e] = x;
+        s += x * x;
+      }
+    s += __shfl_xor(s, 16);
+    s += __shfl_xor(s, 32);
+    ss[xi] = s;
+  }
+  float* red = reinterpret_cast<float*>(smem + 96 * 1024);  // past the pair exchange area
+#pragma unroll
+  for (int xi = 0; xi < FX; ++xi)
+    if (lg == 0) red[((g * 2 + h) * FX + xi) * 16 + lr] = ss[xi];
+  __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  const float* w1 = type == 0 ? fa.qw1 : fa.kw1;
+  uint16_t* const out = type == 0 ? fa.qt : fa.kt;
+#pragma unroll
+  for (int xi = 0; xi < FX; ++xi) {
+    const float tot = ss[xi] + red[((g * 2 + (h ^ 1)) * FX + xi) * 16 + lr];
+    const float r = rsqrtf(tot / (float)D + fa.eps);
+    const int m = m0 + (g * FX + xi) * 16 + lr;
+    float nv[8][4];
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp) {
+      const float4 wv = *reinterpret_cast<const float4*>(w1 + (p0 + pp) * 16 + lg * 4);
+      const float wa[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) nv[pp][e] = rbf((acc[p0 + pp][xi][e] * r) * wa[e]);
+    }
+    if (m >= M) continue;
+#pragma unroll
+    for (int pp = 0; pp < 8; ++pp) {
+      float o[4];
+      const int d = (p0 + pp) * 16 + lg * 4;
+      if (h == 0 && pp < 2 * RDF) {  // the rotate-half RoPE on dims 0..63
+        const uint2 ca = *reinterpret_cast<const uint2*>(fa.cosb + (int64_t)m * fa.RD + d);
+        const uint2 sa = *reinterpret_cast<const uint2*>(fa.sinb + (int64_t)m * fa.RD + d);
+        const float c[4] = {bf2f(ca.x & 0xffffu), bf2f(ca.x >> 16), bf2f(ca.y & 0xffffu), bf2f(ca.y >> 16)};
+        const float sn[4] = {bf2f(sa.x & 0xffffu), bf2f(sa.x >> 16), bf2f(sa.y & 0xffffu), bf2f(sa.y >> 16)};
+        const int q = pp < RDF ? pp + RDF : pp - RDF;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float rh = pp < RDF ? -nv[q][e] : nv[q][e];
+          o[e] = rbf(rbf(nv[pp][e] * c[e]) + rbf(rh * sn[e]));
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = nv[pp][e];
+      }
+      *reinterpret_cast<uint2*>(out + ((int64_t)hh * M + m) * D + d) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+    }
+  }
+}
+
 // REV (two leftover x fragments only): the group walks its W fragments from the last one down, so that its extra
 // fragments (the upper half) come first; the other groups walk upwards. Either way the walk is static code.
 template <int FW, int FX, int XE, int EPI, bool REV>
@@ -258,6 +357,11 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   }
 
   // ------------------------------------------------------------------ epilogue
+  if constexpr (EPI == EPI_FATTN) {
+    static_assert(XE == 0, "the prep epilogue needs whole rows per SIMD group");
+    kx_fattn_epilogue<FW, FX>(p, acc, g, h, lane, m0, n0, smem);
+    return;
+  }
   // lane holds v[e] = y[m][n + e]: m = m0 + 16 xf + lr, n = n0 + 16 wf + 4 lg
 #pragma unroll
   for (int f = 0; f < NACC; ++f) {
@@ -293,6 +397,12 @@ __device__ __forceinline__ void kx_dir(const GemmParams& p) {
 
 template <int FW, int FX, int XE>
 __global__ void __launch_bounds__(512) gemm_kx_kernel(const GemmParams p, const int epi) {
+  if constexpr (FW == 16 && XE == 0) {  // the 256-row tiles also carry the full-attention prep epilogue
+    if (epi == EPI_FATTN) {
+      kx_dir<FW, FX, XE, EPI_FATTN>(p);
+      return;
+    }
+  }
   if (epi == EPI_SILU) kx_dir<FW, FX, XE, EPI_SILU>(p);
   else if (epi == EPI_RESID) kx_dir<FW, FX, XE, EPI_RESID>(p);
   else if (epi == EPI_F32) kx_dir<FW, FX, XE, EPI_F32>(p);
@@ -308,5 +418,7 @@ template __global__ void gemm_kx_kernel<9, 1, 0>(const GemmParams, const int);  
 template __global__ void gemm_kx_kernel<9, 2, 0>(const GemmParams, const int);  // 144 x 128
 template __global__ void gemm_kx_kernel<8, 2, 0>(const GemmParams, const int);  // 128 x 128
 template __global__ void gemm_kx_kernel<8, 1, 0>(const GemmParams, const int);  // 128 x 64
+template __global__ void gemm_kx_kernel<16, 2, 0>(const GemmParams, const int);  // 256 x 128: one head per tile
+template __global__ void gemm_kx_kernel<16, 1, 0>(const GemmParams, const int);  // 256 x 64
 
 }  // namespace ojx

@@ -62,7 +62,18 @@ enum Epi : int {
   EPI_F32 = 1,    // split-K partial: parts[z][m][n] = acc (fp32)
   EPI_RESID = 2,  // h = bf16(residual + bf16(acc))
   EPI_SILU = 3,   // packed gate/up rows -> out = bf16(bf16(silu(bf16 g)) * bf16 u)
-  EPI_COUNT = 4
+  EPI_FATTN = 4,  // full-attention QKV in-projection with the attention prep (K-interleaved 256-row tiles only)
+  EPI_COUNT = 5
+};
+
+// Operands of the full-attention prep epilogue (see fullattn_prep_k in prep.hip for the arithmetic).
+struct FattnParams {
+  const float* qw1; const float* kw1;     // [D] fp32 RMSNorm weights (1 + weight) of q and k heads
+  const uint16_t* cosb; const uint16_t* sinb;  // [M, RD] bf16
+  uint16_t* qt; uint16_t* kt; uint16_t* vt;    // [HQ, M, D], [HKV, M, D], [HKV, M, D]
+  uint16_t* gate;                              // [M, HQ D]
+  int HQ, HKV, RD;
+  float eps;
 };
 
 struct GemmParams {
@@ -77,7 +88,8 @@ struct GemmParams {
   // persistent stream-K kernels (family 5) only
   float* sk_ws;                     // partial-tile slots, 2 per workgroup, BN*BM fp32 each
   int dp_tiles;                     // tiles done whole first (a multiple of the grid)
-  int wpk;                          // 1: W is in the stage-major packed layout (family 6 only; see ojx_pack_weight)
+  int wpk;                          // 1: W is in the stage-major packed layout (see ojx_pack_weight)
+  FattnParams fa;                   // EPI_FATTN only
   int sk_grid;                      // workgroups that share the remaining tiles' K iterations
 };
 
@@ -116,6 +128,10 @@ hipError_t launch_head_gemv(const uint16_t* hn, int64_t rows, const int64_t* las
                             const float* bias, float* scores, int H, hipStream_t st);
 hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_t* packed, int I, int K,
                                hipStream_t st);
+// Full-attention prep from the in-projection output proj [N, (2 HQ + 2 HKV) D], D = 256 (prep.hip).
+hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV, int RD, float eps,
+                                const float* qw1, const float* kw1, const uint16_t* cosb, const uint16_t* sinb,
+                                uint16_t* qt, uint16_t* kt, uint16_t* vt, uint16_t* gate, hipStream_t st);
 // W [N, K] row-major -> packed [K/64][N/16][16][64]: the 16-row x 64-k blocks of one 64-k stage of all rows are
 // contiguous, so a tile's weights for one stage are one contiguous run (N % 16 == 0, K % 64 == 0).
 hipError_t launch_pack_weight(const uint16_t* w, uint16_t* wp, int64_t N, int64_t K, hipStream_t st);

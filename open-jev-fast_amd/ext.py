@@ -320,3 +320,53 @@ def mm_residual_rmsnorm_pk(h, y, wp, w1, rowmask, eps, want_hn=True, cfg=None):
                                              _ptr(rowmask), float(eps), _ptr(h_new), _ptr(hn), M, N, K, _ptr(ws),
                                              nws, _cfgp(cfg), _stream()))
     return h_new, hn
+
+
+# ------------------------------------------------------------------------------------------------ attention prep
+def _prep_outputs(N, HQ, HKV, D, like):
+    qt = torch.empty((HQ, N, D), dtype=torch.bfloat16, device=like.device)
+    kt = torch.empty((HKV, N, D), dtype=torch.bfloat16, device=like.device)
+    vt = torch.empty((HKV, N, D), dtype=torch.bfloat16, device=like.device)
+    gate = torch.empty((N, HQ * D), dtype=torch.bfloat16, device=like.device)
+    return qt, kt, vt, gate
+
+
+def fullattn_prep2(proj, qw1, kw1, cos, sin, B, T, HQ, HKV, D, eps):
+    """The reference extension's fullattn_prep2 (src/kernels.cu:302-360) for B = 1 (the tree forward's call,
+    src/fastmodel.py:462): [qt [1, HQ, T, D], kt [1, HKV, T, D], vt [1, HKV, T, D], gate [T, HQ D]]."""
+    _chk(proj, "proj", torch.bfloat16)
+    _chk(qw1, "qw1", torch.float32)
+    _chk(kw1, "kw1", torch.float32)
+    _chk(cos, "cos", torch.bfloat16)
+    _chk(sin, "sin", torch.bfloat16)
+    if B != 1:
+        raise RuntimeError("fullattn_prep2: B must be 1 (the packed-token forward)")
+    N = proj.shape[0]
+    if N != T or proj.shape[1] != (2 * HQ + 2 * HKV) * D:
+        raise RuntimeError(f"proj {tuple(proj.shape)} does not match T={T}, HQ={HQ}, HKV={HKV}, D={D}")
+    RD = cos.shape[1]
+    qt, kt, vt, gate = _prep_outputs(N, HQ, HKV, D, proj)
+    check(lib().ojx_fullattn_prep(_ptr(proj), N, HQ, HKV, D, RD, float(eps), _ptr(qw1), _ptr(kw1), _ptr(cos),
+                                  _ptr(sin), _ptr(qt), _ptr(kt), _ptr(vt), _ptr(gate), _stream()))
+    return [qt.unsqueeze(0), kt.unsqueeze(0), vt.unsqueeze(0), gate]
+
+
+def mm_fullattn_prep(x, w_qkv, qw1, kw1, cos, sin, HQ, HKV, D, eps):
+    """_mm(hn, d.w_in) + fullattn_prep2 in one kernel (src/fastmodel.py:412,462): the QKV in-projection with the
+    prep in its epilogue. w_qkv row-major [(2 HQ + 2 HKV) D, K] or packed (pack_weight). Returns the prep's outputs
+    [qt [1, HQ, M, D], kt, vt, gate [M, HQ D]]."""
+    _chk(x, "x", torch.bfloat16)
+    for t, nm in ((qw1, "qw1"), (kw1, "kw1")):
+        _chk(t, nm, torch.float32)
+    _chk(cos, "cos", torch.bfloat16)
+    _chk(sin, "sin", torch.bfloat16)
+    M, K = x.shape
+    packed = w_qkv.dim() == 4
+    N, Kw = _pk_shape(w_qkv) if packed else tuple(w_qkv.shape)
+    if Kw != K or N != (2 * HQ + 2 * HKV) * D:
+        raise RuntimeError(f"w_qkv does not match x {tuple(x.shape)}, HQ={HQ}, HKV={HKV}, D={D}")
+    qt, kt, vt, gate = _prep_outputs(M, HQ, HKV, D, x)
+    check(lib().ojx_gemm_qkv_fullattn_prep(_ptr(x), _ptr(w_qkv), int(packed), _ptr(qw1), _ptr(kw1), _ptr(cos),
+                                           _ptr(sin), _ptr(qt), _ptr(kt), _ptr(vt), _ptr(gate), M, K, HQ, HKV, D,
+                                           cos.shape[1], float(eps), _stream()))
+    return [qt.unsqueeze(0), kt.unsqueeze(0), vt.unsqueeze(0), gate]

@@ -17,6 +17,9 @@ What it restates (reference file:line):
   pack_gate_up       the fused-GEMM weight layout (rows in blocks of 8: 4 gate rows, 4 up rows) — libojx's own
                      layout, restated here so tests can build it on the CPU
   pack_weight        the stage-major packed weight layout of the *_pk projections (libojx's own), likewise
+  fullattn_prep      fullattn_prep2_k (src/kernels.cu:302-355) for B = 1, the full-attention consumer of the QKV
+                     in-projection (src/fastmodel.py:462): per-head RMSNorm + rotate-half RoPE of q / k, v and gate
+                     copied, in the head-major output layout; fullattn_prep_f64 is its fp64 check
   linear_f64         fp64 brute-force dot products (numpy), the independent check the oracle is pinned against
   head_scores        mdl.head(hn[lastidx].float()).squeeze(-1) (src/server.py:37, 57, 129; hn[lastidx] at
                      src/fastmodel.py:314, 482) for a Linear(H, 1) with fp32 weight and bias: torch fp32 on the CPU.
@@ -126,6 +129,54 @@ def pack_weight(w):
     packed[s, b, r, c] = W[16 b + r, 64 s + c] (libojx's own layout, so that tests can build it on the CPU)."""
     N, K = w.shape
     return w.reshape(N // 16, 16, K // 64, 64).permute(2, 0, 1, 3).contiguous()
+
+
+def fullattn_prep(proj, qw1, kw1, cos, sin, HQ, HKV, D, eps):
+    """fullattn_prep2_k (src/kernels.cu:302-355) for B = 1: proj [N, (2 HQ + 2 HKV) D] bf16 -> (qt [HQ, N, D],
+    kt [HKV, N, D], vt [HKV, N, D], gate [N, HQ D]). q/k heads: xn = bf16((x * rsqrt(sum x^2 / D + eps)) * w1),
+    then on the first RD = cos.shape[1] dims out = bf16(bf16(xn * cos) + bf16(rh * sin)), rh = -xn[d + RD/2] for
+    d < RD/2 and xn[d - RD/2] above; v and gate copied."""
+    N = proj.shape[0]
+    RD = cos.shape[1]
+    p = proj.float().view(N, -1)
+    q_g = p[:, :2 * HQ * D].view(N, HQ, 2, D)
+    q, gate = q_g[:, :, 0], q_g[:, :, 1]
+    k = p[:, 2 * HQ * D:2 * HQ * D + HKV * D].view(N, HKV, D)
+    v = p[:, 2 * HQ * D + HKV * D:].view(N, HKV, D)
+
+    def norm_rope(x, w1):
+        r = torch.rsqrt((x * x).sum(-1, keepdim=True) / D + eps)
+        xn = _bf16((x * r) * w1.float()).float()
+        c, s = cos.float()[:, None, :], sin.float()[:, None, :]
+        a, b = xn[..., :RD // 2], xn[..., RD // 2:RD]
+        rot = torch.cat([-b, a], -1)
+        head = _bf16(_bf16(xn[..., :RD] * c).float() + _bf16(rot * s).float()).float()
+        return _bf16(torch.cat([head, xn[..., RD:]], -1))
+
+    qt = norm_rope(q, qw1).permute(1, 0, 2).contiguous()
+    kt = norm_rope(k, kw1).permute(1, 0, 2).contiguous()
+    return qt, kt, _bf16(v).permute(1, 0, 2).contiguous(), _bf16(gate).reshape(N, HQ * D)
+
+
+def fullattn_prep_f64(proj, qw1, kw1, cos, sin, HQ, HKV, D, eps):
+    """fp64 numpy form of fullattn_prep without the intermediate bf16 roundings (the independent check)."""
+    N = proj.shape[0]
+    RD = cos.shape[1]
+    p = proj.float().numpy().astype(np.float64).reshape(N, -1)
+    c, s = cos.float().numpy().astype(np.float64), sin.float().numpy().astype(np.float64)
+    out = []
+    for base, heads, w1, stride in ((0, HQ, qw1, 2 * D), (2 * HQ * D, HKV, kw1, D)):
+        w = w1.double().numpy()
+        o = np.zeros((heads, N, D))
+        for h in range(heads):
+            x = p[:, base + h * stride: base + h * stride + D]
+            xn = x / np.sqrt((x * x).sum(1, keepdims=True) / D + eps) * w
+            y = xn.copy()
+            y[:, :RD // 2] = xn[:, :RD // 2] * c[:, :RD // 2] - xn[:, RD // 2:RD] * s[:, :RD // 2]
+            y[:, RD // 2:RD] = xn[:, RD // 2:RD] * c[:, RD // 2:] + xn[:, :RD // 2] * s[:, RD // 2:]
+            o[h] = y
+        out.append(o)
+    return out[0], out[1]
 
 
 def head_scores(hn, lastidx, w, bias=None):

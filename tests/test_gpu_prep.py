@@ -1,0 +1,118 @@
+"""GPU parity of the full-attention prep (the consumer of the full-attention layers' QKV in-projection), through
+the C-ABI.
+
+* ojx_fullattn_prep (the reference's K.fullattn_prep2, src/kernels.cu:302-355) against the oracle's restatement:
+  v and gate bit for bit; q and k within one bf16 rounding step, because the per-row sum of squares is added in a
+  different order (wave butterfly vs the oracle's torch sum) and may move one rsqrt across a rounding boundary.
+* ojx_gemm_qkv_fullattn_prep (the in-projection GEMM with the prep in its epilogue), row-major and packed weights:
+  its projection is the kx tile's own, so it is checked against (a) the oracle chain GEMM -> prep on the north
+  star's tolerance and (b) the unfused chain ext.mm with the same tile -> ojx_fullattn_prep, which must agree to
+  within one rounding step (same products, same K order, only the sum-of-squares order differs).
+
+Tolerance: max |out - ref| / max |ref| <= 1e-2 and mean |out - ref| <= 1e-3 * RMS(ref).
+"""
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+TOL = dict(max_rel=1e-2, mean_abs_rms=1e-3)
+EPS = 1e-6
+
+
+def _say(*a):
+    print(*a, flush=True)
+
+
+def _assert_tol(O, out, ref, what):
+    ok, a, b = O.tolerance_ok(out.float().cpu(), ref.float().cpu(), **TOL)
+    assert ok, f"{what}: max_rel {a:.3e} mean/rms {b:.3e}"
+
+
+def _inputs(N, HQ, HKV, D, RD, seed, K=None):
+    g = torch.Generator().manual_seed(seed)
+    qw1 = (1.0 + 0.1 * torch.randn(D, generator=g)).float()
+    kw1 = (1.0 + 0.1 * torch.randn(D, generator=g)).float()
+    ang = torch.rand(N, RD // 2, generator=g) * 6.0
+    cos = torch.cat([ang.cos(), ang.cos()], 1).bfloat16()
+    sin = torch.cat([ang.sin(), ang.sin()], 1).bfloat16()
+    P = (2 * HQ + 2 * HKV) * D
+    if K is None:
+        return torch.randn(N, P, generator=g).bfloat16(), qw1, kw1, cos, sin
+    x = torch.randn(N, K, generator=g).bfloat16()
+    w = (torch.randn(P, K, generator=g) * K ** -0.5).bfloat16()
+    return x, w, qw1, kw1, cos, sin
+
+
+def _close_bf16(got, want, what):
+    """Within one bf16 rounding step of the value or of the row's largest term, and mostly exact."""
+    g, w = got.float().cpu(), want.float().cpu()
+    err = (g - w).abs()
+    # one step of a RoPE term is relative to the row's magnitude, not to the (possibly cancelled) sum
+    bound = (w.abs() + w.abs().amax(-1, keepdim=True)) * 2.0 ** -7
+    assert bool((err <= bound).all()), f"{what}: worst {(err - bound).max().item():.3e} above the bound"
+    frac = (err == 0).float().mean().item()
+    assert frac > 0.9, f"{what}: only {frac:.3f} of the values equal"
+
+
+@pytest.mark.parametrize("N,HQ,HKV,RD", [(1, 24, 4, 64), (7, 24, 4, 64), (130, 3, 2, 64), (33, 2, 1, 32),
+                                         (5, 1, 1, 128)])
+def test_fullattn_prep_vs_oracle(ext, O, dev, N, HQ, HKV, RD):
+    D = 256
+    _say(f"case prep N={N} HQ={HQ} HKV={HKV} RD={RD}")
+    proj, qw1, kw1, cos, sin = _inputs(N, HQ, HKV, D, RD, seed=N + HQ + RD)
+    qt, kt, vt, gate = ext.fullattn_prep2(proj.to(dev), qw1.to(dev), kw1.to(dev), cos.to(dev), sin.to(dev), 1, N,
+                                          HQ, HKV, D, EPS)
+    torch.cuda.synchronize()
+    rq, rk, rv, rg = O.fullattn_prep(proj, qw1, kw1, cos, sin, HQ, HKV, D, EPS)
+    assert tuple(qt.shape) == (1, HQ, N, D) and tuple(kt.shape) == (1, HKV, N, D)
+    assert tuple(vt.shape) == (1, HKV, N, D) and tuple(gate.shape) == (N, HQ * D)
+    assert torch.equal(vt[0].cpu(), rv) and torch.equal(gate.cpu(), rg)
+    _close_bf16(qt[0], rq, "q")
+    _close_bf16(kt[0], rk, "k")
+
+
+def test_fullattn_prep_rejects(ext, dev):
+    proj, qw1, kw1, cos, sin = [t.to(dev) for t in _inputs(3, 2, 1, 256, 64, seed=1)]
+    with pytest.raises(RuntimeError):
+        ext.fullattn_prep2(proj, qw1, kw1, cos, sin, 2, 3, 2, 1, 256, EPS)  # B != 1
+    with pytest.raises(RuntimeError):
+        ext.fullattn_prep2(proj, qw1, kw1, cos[:, :48].contiguous(), sin[:, :48].contiguous(), 1, 3, 2, 1, 256, EPS)
+    empty = torch.empty(0, proj.shape[1], dtype=proj.dtype, device=dev)
+    out = ext.fullattn_prep2(empty, qw1, kw1, cos[:0], sin[:0], 1, 0, 2, 1, 256, EPS)
+    assert out[0].shape[2] == 0
+
+
+# (M, HQ, HKV, K): the north star's full-attention in-projection is HQ = 24, HKV = 4, K = 5120 (N = 14336); smaller
+# head counts and K keep the ragged-M cases quick.
+@pytest.mark.parametrize("M,HQ,HKV,K", [(1, 2, 1, 256), (7, 24, 4, 5120), (64, 3, 2, 640), (65, 3, 2, 640),
+                                        (200, 2, 1, 1024), (288, 24, 4, 5120)])
+@pytest.mark.parametrize("packed", [False, True])
+def test_gemm_qkv_fullattn_prep(pkg, ext, O, dev, M, HQ, HKV, K, packed):
+    D, RD = 256, 64
+    _say(f"case fused prep M={M} HQ={HQ} HKV={HKV} K={K} packed={packed}")
+    x, w, qw1, kw1, cos, sin = _inputs(M, HQ, HKV, D, RD, seed=M + K + HQ, K=K)
+    xd, wd = x.to(dev), w.to(dev)
+    qd, kd, cd, sd = qw1.to(dev), kw1.to(dev), cos.to(dev), sin.to(dev)
+    wuse = ext.pack_weight(wd) if packed else wd
+    qt, kt, vt, gate = ext.mm_fullattn_prep(xd, wuse, qd, kd, cd, sd, HQ, HKV, D, EPS)
+    # (b) the unfused chain with the same tile: the projection is identical, the prep's sum order differs
+    tile = 89 if M <= 64 else 88
+    proj = (ext.mm_pk if packed else ext.mm)(xd, wuse, cfg=(tile, 1))
+    uq, uk, uv, ug = ext.fullattn_prep2(proj, qd, kd, cd, sd, 1, M, HQ, HKV, D, EPS)
+    torch.cuda.synchronize()
+    assert torch.equal(vt.cpu(), uv.cpu()) and torch.equal(gate.cpu(), ug.cpu())
+    _close_bf16(qt[0], uq[0], "fused q vs unfused")
+    _close_bf16(kt[0], uk[0], "fused k vs unfused")
+    # (a) the oracle chain on the north star's tolerance
+    rq, rk, rv, rg = O.fullattn_prep(O.linear_bf16(x, w), qw1, kw1, cos, sin, HQ, HKV, D, EPS)
+    for got, ref, nm in ((qt[0], rq, "q"), (kt[0], rk, "k"), (vt[0], rv, "v"), (gate, rg, "gate")):
+        _assert_tol(O, got, ref, f"{nm} M={M}")
+
+
+def test_gemm_qkv_fullattn_prep_rejects(ext, dev):
+    x, w, qw1, kw1, cos, sin = [t.to(dev) for t in _inputs(4, 2, 1, 256, 32, seed=2, K=256)]
+    with pytest.raises(RuntimeError):  # the fused epilogue handles RD = 64 only
+        ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, 2, 1, 256, EPS)
+    with pytest.raises(RuntimeError):  # weight rows do not match the head counts
+        ext.mm_fullattn_prep(x, w[:512].contiguous(), qw1, kw1, cos, sin, 2, 1, 256, EPS)

@@ -245,3 +245,54 @@ def test_pack_weight_layout_bruteforce():
             for r in range(16):
                 for c in range(64):
                     assert int(p[s, b, r, c]) == int(bits[16 * b + r, 64 * s + c])
+
+
+def _prep_inputs(N, HQ, HKV, D, RD, seed):
+    g = torch.Generator().manual_seed(seed)
+    proj = torch.randn(N, (2 * HQ + 2 * HKV) * D, generator=g).bfloat16()
+    qw1 = (1.0 + 0.1 * torch.randn(D, generator=g)).float()
+    kw1 = (1.0 + 0.1 * torch.randn(D, generator=g)).float()
+    ang = torch.rand(N, RD // 2, generator=g) * 6.0
+    cos = torch.cat([ang.cos(), ang.cos()], 1).bfloat16()
+    sin = torch.cat([ang.sin(), ang.sin()], 1).bfloat16()
+    return proj, qw1, kw1, cos, sin
+
+
+def test_fullattn_prep_vs_f64():
+    HQ, HKV, D, RD = 3, 2, 256, 64
+    proj, qw1, kw1, cos, sin = _prep_inputs(5, HQ, HKV, D, RD, 1)
+    qt, kt, vt, gate = O.fullattn_prep(proj, qw1, kw1, cos, sin, HQ, HKV, D, 1e-6)
+    q64, k64 = O.fullattn_prep_f64(proj, qw1, kw1, cos, sin, HQ, HKV, D, 1e-6)
+    for got, want in ((qt, q64), (kt, k64)):
+        err = np.abs(got.float().numpy() - want)
+        # three bf16 roundings along the way, and the RoPE sum of two rounded terms can cancel: within 2^-6 of the
+        # row's largest value (a wrong sign or partner index is off by O(1))
+        scale = np.abs(want).max(-1, keepdims=True)
+        assert (err <= scale * 2.0 ** -6).all(), (err / scale).max()
+        assert np.median(err / scale) < 2.0 ** -9
+
+
+def test_fullattn_prep_rotation_and_copies_exact():
+    """cos = 1, sin = 0 leaves the normalised head; cos = 0, sin = 1 gives rotate_half of it: out[d] =
+    -xn[d + RD/2] below RD/2 and xn[d - RD/2] up to RD (the sign and the partner index); dims >= RD and the copied
+    v / gate heads sit where the reference's indexing puts them (checked element by element)."""
+    HQ, HKV, D, RD, N = 2, 1, 256, 64, 3
+    proj, qw1, kw1, _, _ = _prep_inputs(N, HQ, HKV, D, RD, 2)
+    one, zero = torch.ones(N, RD).bfloat16(), torch.zeros(N, RD).bfloat16()
+    q1, k1, v, gate = O.fullattn_prep(proj, qw1, kw1, one, zero, HQ, HKV, D, 1e-6)
+    q2, k2, _, _ = O.fullattn_prep(proj, qw1, kw1, zero, one, HQ, HKV, D, 1e-6)
+    for a, b in ((q1, q2), (k1, k2)):
+        assert torch.equal(b[..., :RD // 2], -a[..., RD // 2:RD])
+        assert torch.equal(b[..., RD // 2:RD], a[..., :RD // 2])
+        assert torch.equal(b[..., RD:], a[..., RD:])
+    P = (2 * HQ + 2 * HKV) * D
+    for n in range(N):
+        for h in range(HQ):
+            assert torch.equal(gate[n, h * D:(h + 1) * D], proj[n, 2 * h * D + D: 2 * h * D + 2 * D])
+        for h in range(HKV):
+            assert torch.equal(v[h, n], proj[n, 2 * HQ * D + HKV * D + h * D: 2 * HQ * D + HKV * D + (h + 1) * D])
+    assert P == proj.shape[1]
+    # constant rows: x = 2 everywhere, unit weights, eps 0 -> xn = 1 exactly
+    c = torch.full((1, P), 2.0).bfloat16()
+    qc, kc, _, _ = O.fullattn_prep(c, torch.ones(D), torch.ones(D), one[:1], zero[:1], HQ, HKV, D, 0.0)
+    assert bool((qc == 1.0).all()) and bool((kc == 1.0).all())
