@@ -12,7 +12,8 @@ per-shape table at M = 7 / 64 / 288 / 539 / 2048 for the five projection shapes.
 
 Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
 the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV), --vs-hipblaslt
-(each planned call against torch F.linear on the same box).
+(each planned call against torch F.linear on the same box), --prep (the full-attention in-projection with its prep:
+two launches against the fused epilogue).
 """
 import argparse
 import json
@@ -321,6 +322,70 @@ def main_head(args, pkg, ext, perf):
                           "frac": round(nbytes / perf.HBM_PEAK / t, 4)}), flush=True)
 
 
+def main_prep(args, pkg, ext, perf):
+    """The full-attention in-projection and its prep (src/fastmodel.py:412,462): the planned GEMM followed by
+    ojx_fullattn_prep (two launches) against ojx_gemm_qkv_fullattn_prep (the prep in the GEMM's epilogue), HQ = 24,
+    HKV = 4, D = 256, RoPE dims 64, K = 5120. Each timed as a HIP graph of 10 calls over rotating weight copies."""
+    dev = "cuda"
+    HQ, HKV, D, RD, K = 24, 4, 256, 64, 5120
+    N = (2 * HQ + 2 * HKV) * D
+    Ms = [int(m) for m in args.m.split(",")] if args.m else [7, 64, 288, 539, 2048]
+    ws = make_weights(N, K, perf.copies_for(N * K * 2), seed=11)
+    qw1 = torch.ones(D, device=dev)
+    kw1 = torch.ones(D, device=dev)
+    for M in Ms:
+        x = torch.randn(M, K, device=dev).bfloat16()
+        ang = torch.rand(M, RD // 2, device=dev) * 6.0
+        cos = torch.cat([ang.cos(), ang.cos()], 1).bfloat16()
+        sin = torch.cat([ang.sin(), ang.sin()], 1).bfloat16()
+        proj = ext.mm(x, ws[0])
+        two = [lambda w=w: ext.fullattn_prep2(ext.mm(x, w), qw1, kw1, cos, sin, 1, M, HQ, HKV, D, 1e-6) for w in ws]
+        fused = [lambda w=w: ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, HQ, HKV, D, 1e-6) for w in ws]
+        gemm = [lambda w=w: ext.mm(x, w) for w in ws]
+        prep = [lambda: ext.fullattn_prep2(proj, qw1, kw1, cos, sin, 1, M, HQ, HKV, D, 1e-6)]
+        t = {k: min(perf.gpu_time(f, iters=10, reps=3), perf.gpu_time(f, iters=10, reps=3))
+             for k, f in (("gemm", gemm), ("prep", prep), ("two_launch", two), ("fused", fused))}
+        print(json.dumps({"prep": "full-attention in-projection + prep", "M": M, "N": N, "K": K,
+                          **{k + "_us": round(v * 1e6, 1) for k, v in t.items()},
+                          "prep_roof_us": round(4 * M * N / perf.HBM_PEAK * 1e6, 2)}), flush=True)
+    del ws
+    # linear-attention prep on a tree of S candidate paths: a shared prompt of Lr rows, then one leaf of lf rows per
+    # path (the packed rows are the prompt and the leaves; every prompt row is written to S slots)
+    import numpy as np
+    HK, HV, HD = 16, 48, 128
+    KD, VD = HK * HD, HV * HD
+    C, P = 2 * KD + VD, 2 * KD + 2 * VD + 2 * HV
+    for Lr, S, lf in ((200, 8, 11), (480, 8, 7), (1800, 16, 15)):
+        N = -(-(Lr + S * lf) // 32) * 32
+        L2 = -(-(Lr + lf) // 16) * 16
+        src = np.full((S, L2), -1, np.int32)
+        for c in range(S):
+            src[c, :Lr] = np.arange(Lr)
+            src[c, Lr:Lr + lf] = Lr + c * lf + np.arange(lf)
+        flat = src.reshape(-1)
+        grp = np.where(flat >= 0, flat, N)
+        rep_pos = np.argsort(grp, kind="stable").astype(np.int32)
+        rep_ptr = np.concatenate([[0], np.cumsum(np.bincount(grp, minlength=N + 1))]).astype(np.int32)
+        hist = np.full((N + 1, 4), -1, np.int32)
+        for c in range(S):
+            for t_ in range(Lr + lf):
+                hist[src[c, t_]] = [src[c, t_ - 3 + i] if t_ - 3 + i >= 0 else -1 for i in range(4)]
+        d = lambda a: torch.as_tensor(a).to(dev).contiguous()  # noqa: E731
+        proj = torch.randn(N, P, device=dev).bfloat16()
+        convw = (torch.randn(C, 4, device=dev) * 0.5).bfloat16()
+        A_log = torch.randn(HV, device=dev).bfloat16()
+        dt_bias = torch.randn(HV, device=dev).bfloat16()
+        args = (proj, d(hist), d(rep_ptr), d(rep_pos), L2, convw, A_log, dt_bias, KD, VD, HV, HK, HD, False)
+        fn = [lambda: ext.linattn_prep_dedup2(*args)]
+        tl = min(perf.gpu_time(fn, iters=10, reps=3), perf.gpu_time(fn, iters=10, reps=3))
+        R = S * L2
+        nbytes = (Lr + S * lf) * (C + 2 * HV) * 2 + C * 8 + R * (C * 2 + HV * 6)   # rows read once, slots written
+        print(json.dumps({"prep": "linear-attention prep (tree layout)", "rows": Lr + S * lf, "paths": S, "slots": R,
+                          "us": round(tl * 1e6, 1), "gbs": round(nbytes / tl / 1e9, 1),
+                          "roof_us": round(nbytes / perf.HBM_PEAK * 1e6, 2),
+                          "frac": round(nbytes / perf.HBM_PEAK / tl, 3)}), flush=True)
+
+
 def main_vs_hipblaslt(args, pkg, ext, perf):
     """This build's planned call against torch F.linear (hipBLASLt) on the same box, in one process: each timed as a
     HIP graph of 10 calls over the same rotating weight copies (perf.gpu_time), best of two measurements. The ojx
@@ -361,6 +426,7 @@ def main():
     ap.add_argument("--stack", action="store_true")
     ap.add_argument("--head", action="store_true")
     ap.add_argument("--vs-hipblaslt", action="store_true")
+    ap.add_argument("--prep", action="store_true")
     ap.add_argument("--m", default="")
     ap.add_argument("--shapes", default="")
     ap.add_argument("--no-cpu", action="store_true")
@@ -386,6 +452,8 @@ def main():
         main_head(args, pkg, ext, perf)
     elif args.vs_hipblaslt:
         main_vs_hipblaslt(args, pkg, ext, perf)
+    elif args.prep:
+        main_prep(args, pkg, ext, perf)
     else:
         main_default(args, pkg, ext, perf)
 

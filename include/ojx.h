@@ -159,6 +159,21 @@ int ojx_gemm_qkv_fullattn_prep(const void* x, const void* w, int32_t w_packed, c
                                int64_t M, int64_t K, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
                                ojx_stream_t stream);
 
+/* Linear-attention prep on the tree layout, the consumer of the linear-attention layers' in-projection: replaces
+ * linattn_prep_dedup2 (src/kernels.cu:1176-1290; called as K.linattn_prep_dedup2(proj, lay.hist, lay.rep_ptr,
+ * lay.rep_pos, lay.L2, convw, A_log, dt_bias, KD, VD, HV, HK, HD, rep_qk) by forward_gtree, src/fastmodel.py:420,438).
+ * proj [N, 2 KD + 2 VD + 2 HV] bf16 (q | k | v conv channels, z, b, a); hist int32 [N + 1, 4] (rows t-3 .. t of each
+ * packed row's path, -1 = none; row N unused), rep_ptr int32 [N + 2] and rep_pos int32 [R] (the CSR map from packed
+ * rows to path slots, group N = end padding), convw bf16 [2 KD + VD, 4], A_log and dt_bias bf16 [HV]. Outputs:
+ * q, k bf16 [R, RQ KD] with RQ = HV / HK (3) when rep_qk != 0 else 1, v bf16 [R, VD], g fp32 [R, HV], beta bf16
+ * [R, HV]. Depthwise causal conv (4 taps) + SiLU, L2 norm of each q / k head, beta = sigmoid(b),
+ * g = -exp(A_log) softplus(a + dt_bias); each packed row computed once and written to every slot holding it; the
+ * end-padding slots get zeros. HD = 128, KD = HK HD, R a multiple of L2, HV <= 256; every pointer 16-byte aligned. */
+int ojx_linattn_prep(const void* proj, const int32_t* hist, const int32_t* rep_ptr, const int32_t* rep_pos,
+                     int64_t N, int64_t R, int64_t L2, const void* convw, const void* A_log, const void* dt_bias,
+                     int32_t KD, int32_t VD, int32_t HV, int32_t HK, int32_t HD, int32_t rep_qk, void* q, void* k,
+                     void* v, float* g, void* beta, ojx_stream_t stream);
+
 /* Bytes of the static device scratch behind ojx_gemm_residual_rmsnorm_noalloc (one array per GPU). */
 #define OJX_NOALLOC_SCRATCH_BYTES (32LL << 20)
 

@@ -54,6 +54,8 @@ EXPORTS = {
     "ojx_fullattn_prep": (ctypes.c_int, [_p, _i64, _i32, _i32, _i32, _i32, _f32, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "ojx_gemm_qkv_fullattn_prep": (ctypes.c_int, [_p, _p, _i32, _p, _p, _p, _p, _p, _p, _p, _p, _i64, _i64, _i32,
                                                   _i32, _i32, _i32, _f32, _p]),
+    "ojx_linattn_prep": (ctypes.c_int, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                                        _i32, _p, _p, _p, _p, _p, _p]),
     "ojx_add_rmsnorm": (ctypes.c_int, [_p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _p]),
     "ojx_add_rmsnorm_sk": (ctypes.c_int, [_p, _p, _i32, _p, _p, _f32, _p, _p, _i64, _i64, _p]),
     "ojx_silu_mul": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),

@@ -635,6 +635,36 @@ int ojx_gemm_qkv_fullattn_prep(const void* x, const void* w, int32_t w_packed, c
               nullptr, 0, nullptr, nullptr, 0.f, nullptr, w_packed != 0, &fa);
 }
 
+int ojx_linattn_prep(const void* proj, const int32_t* hist, const int32_t* rep_ptr, const int32_t* rep_pos,
+                     int64_t N, int64_t R, int64_t L2, const void* convw, const void* A_log, const void* dt_bias,
+                     int32_t KD, int32_t VD, int32_t HV, int32_t HK, int32_t HD, int32_t rep_qk, void* q, void* k,
+                     void* v, float* g, void* beta, ojx_stream_t stream) {
+  if (HD != 128) return fail(OJX_ERR_SHAPE, "linear-attention prep supports head_dim 128 (HD=%d)", HD);
+  if (HK < 1 || HK * HD != KD) return fail(OJX_ERR_SHAPE, "KD=%d must be HK * HD (HK=%d)", KD, HK);
+  if (HV < 1 || HV > 256 || VD < 8 || VD % 8 != 0)
+    return fail(OJX_ERR_SHAPE, "bad value dims VD=%d HV=%d (HV <= 256, VD a multiple of 8)", VD, HV);
+  const int rq = rep_qk ? HV / HK : 1;
+  if (rq != 1 && rq != 3) return fail(OJX_ERR_SHAPE, "replicated q/k needs HV / HK = 3 (HV=%d HK=%d)", HV, HK);
+  if (N < 0 || N >= (1LL << 31) - 1 || R < 0 || R >= (1LL << 31) || L2 < 1 || R % L2 != 0)
+    return fail(OJX_ERR_SHAPE, "bad sizes N=%lld R=%lld L2=%lld (R a multiple of L2)", (long long)N, (long long)R,
+                (long long)L2);
+  if (N + (R + 15) / 16 > 65535) return fail(OJX_ERR_SHAPE, "N + R/16 = %lld rows of workgroups exceeds 65535",
+                                             (long long)(N + (R + 15) / 16));
+  if (R == 0) return OJX_OK;
+  const void* ptrs[] = {proj, hist, rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta};
+  for (const void* p : ptrs)
+    if (p == nullptr) return fail(OJX_ERR_ARG, "linear-attention prep operands must be non-null");
+  const void* vec[] = {proj, hist, convw, q, k, v};
+  for (const void* p : vec)
+    if (!aligned(p, 16)) return fail(OJX_ERR_ARG, "proj, hist, convw, q, k and v must be 16-byte aligned");
+  return hip_check(ojx::launch_linattn_prep(static_cast<const uint16_t*>(proj), hist, rep_ptr, rep_pos, N, R,
+                                            static_cast<const uint16_t*>(convw), static_cast<const uint16_t*>(A_log),
+                                            static_cast<const uint16_t*>(dt_bias), KD, VD, HV, rq,
+                                            static_cast<uint16_t*>(q), static_cast<uint16_t*>(k),
+                                            static_cast<uint16_t*>(v), g, static_cast<uint16_t*>(beta),
+                                            static_cast<hipStream_t>(stream)), "linear-attention prep launch");
+}
+
 int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* residual, const float* w1,
                                       const int32_t* rowmask, float eps, void* h_out, void* hn_out, int64_t M,
                                       int64_t N, int64_t K, const ojx_cfg* cfg, ojx_stream_t stream) {

@@ -55,10 +55,13 @@ struct KxShape {
 // rotate-half RoPE on the first RD = 64 dims (the partner of dim d is in fragment d/16 +- 2 of the same lane),
 // stored head-major; gate and v: proj stored as it is. Same arithmetic as fullattn_prep_k (prep.hip), the
 // reference's fullattn_prep2_k (src/kernels.cu:302-355), except the order in which the sum of squares is added.
-template <int FW, int FX>
-__device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&acc)[FW][FX], int g, int h, int lane,
+// H is the wave's half as a template argument: the accumulators are then indexed by constants and stay in registers
+// (an index computed from the wave id would put the whole array on the stack).
+template <int FW, int FX, int H>
+__device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&acc)[FW][FX], int g, int lane,
                                                   int m0, int n0, uint8_t* smem) {
   static_assert(FW == 16, "one 256-dim head per tile");
+  constexpr int h = H;
   constexpr int D = 256, RDF = 2;  // RoPE dims = 64 = 4 fragments; partner fragment distance 2
   const FattnParams& fa = p.fa;
   const int lr = lane & 15, lg = lane >> 4;
@@ -66,7 +69,7 @@ __device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&a
   const int type = cb < 2 * fa.HQ ? (cb & 1) : (cb < 2 * fa.HQ + fa.HKV ? 2 : 3);  // 0 q, 1 gate, 2 k, 3 v
   const int hh = cb < 2 * fa.HQ ? cb >> 1 : (type == 2 ? cb - 2 * fa.HQ : cb - 2 * fa.HQ - fa.HKV);
   const int M = p.M;
-  const int p0 = h * 8;  // this wave's fragments (positions = W fragments) p0 .. p0+7
+  constexpr int p0 = h * 8;  // this wave's fragments (positions = W fragments) p0 .. p0+7
   if (type == 1 || type == 3) {
 #pragma unroll
     for (int pp = 0; pp < 8; ++pp)
@@ -359,7 +362,8 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   // ------------------------------------------------------------------ epilogue
   if constexpr (EPI == EPI_FATTN) {
     static_assert(XE == 0, "the prep epilogue needs whole rows per SIMD group");
-    kx_fattn_epilogue<FW, FX>(p, acc, g, h, lane, m0, n0, smem);
+    if (h == 0) kx_fattn_epilogue<FW, FX, 0>(p, acc, g, lane, m0, n0, smem);
+    else kx_fattn_epilogue<FW, FX, 1>(p, acc, g, lane, m0, n0, smem);
     return;
   }
   // lane holds v[e] = y[m][n + e]: m = m0 + 16 xf + lr, n = n0 + 16 wf + 4 lg

@@ -132,6 +132,10 @@ hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_
 hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV, int RD, float eps,
                                 const float* qw1, const float* kw1, const uint16_t* cosb, const uint16_t* sinb,
                                 uint16_t* qt, uint16_t* kt, uint16_t* vt, uint16_t* gate, hipStream_t st);
+hipError_t launch_linattn_prep(const uint16_t* proj, const int32_t* hist, const int32_t* rep_ptr,
+                               const int32_t* rep_pos, int64_t N, int64_t R, const uint16_t* convw,
+                               const uint16_t* A_log, const uint16_t* dt_bias, int KD, int VD, int HV, int RQ,
+                               uint16_t* q, uint16_t* k, uint16_t* v, float* g, uint16_t* beta, hipStream_t st);
 // W [N, K] row-major -> packed [K/64][N/16][16][64]: the 16-row x 64-k blocks of one 64-k stage of all rows are
 // contiguous, so a tile's weights for one stage are one contiguous run (N % 16 == 0, K % 64 == 0).
 hipError_t launch_pack_weight(const uint16_t* w, uint16_t* wp, int64_t N, int64_t K, hipStream_t st);

@@ -95,4 +95,135 @@ hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV
   return hipGetLastError();
 }
 
+// Linear-attention prep on the tree layout: the consumer of the linear-attention layers' in-projection.
+//
+// Reference: linattn_prep_dedup2_k (src/kernels.cu:1176-1265), called from forward_gtree as
+// K.linattn_prep_dedup2(proj, lay.hist, lay.rep_ptr, lay.rep_pos, lay.L2, convw, A_log, dt_bias, KD, VD, HV, HK, HD,
+// rep_qk) (src/fastmodel.py:420,438). proj [N, P] bf16, P = C + VD + 2 HV with C = 2 KD + VD conv channels
+// (q | k | v), then the z gate (VD, read later by the gated norm), then b [HV] and a [HV]. Each packed row n is
+// computed once and written to every slot s = rep_pos[p], p in [rep_ptr[n], rep_ptr[n+1]) (the candidate paths that
+// contain it); the slots of group N (rep_ptr[N] .. rep_ptr[N+1]) are the paths' end padding and receive zeros.
+//   channel c: conv = sum_{i=0..3} convw[c][i] * proj[hist[n][i]][c] in that order (hist[n] = the rows t-3 .. t on
+//   the row's path, -1 = none), o = bf16(silu(conv)); q and k channels (c < 2 KD) are then L2-normalised over their
+//   head of HD = 128 channels: o * (1 / sqrt(sum o^2 + 1e-6)), the sum added by a butterfly over 16 lanes of 8
+//   channels each (xor 8, 4, 2, 1, each lane's 8 squares added in order first), and rounded to bf16.
+//   head h < HV: beta = bf16(sigmoid(b_h)), g = -exp(A_log[h]) * softplus(a_h + dt_bias[h]) (fp32, softplus(x) = x
+//   above 20).
+//   Outputs: q, k [R, RQ HK HD] (RQ = 1, or 3 = HV / HK copies of each head side by side), v [R, VD], g [R, HV] fp32,
+//   beta [R, HV] bf16; R = rep_pos's length.
+//
+// Layout of the work: a workgroup of 256 lanes takes 2048 channels of one packed row (each lane 8 consecutive
+// channels, one 16-byte load per history row, 16 lanes = one q/k head), computes them once and stores them to each of
+// the row's slots (a wave writes 1 KB contiguous per slot). Workgroups with y >= N write the end-padding slots,
+// 16 slots each. Products of two bf16 values are exact in fp32, so the conv's sum is the only rounding order that
+// matters, and it is kept.
+template <int RQ>
+__global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict__ proj, const int4* __restrict__ hist,
+                                                     const int* __restrict__ rep_ptr, const int* __restrict__ rep_pos,
+                                                     const uint16_t* __restrict__ convw,
+                                                     const uint16_t* __restrict__ A_log,
+                                                     const uint16_t* __restrict__ dt_bias, uint16_t* __restrict__ q,
+                                                     uint16_t* __restrict__ k, uint16_t* __restrict__ v,
+                                                     float* __restrict__ g, uint16_t* __restrict__ beta, int N, int KD,
+                                                     int VD, int HV) {
+  constexpr int HD = 128;
+  const int C = 2 * KD + VD;
+  const int64_t P = (int64_t)C + VD + 2 * HV;
+  const int n = blockIdx.y;
+  const bool pad = n >= N;
+  int p0, p1;
+  if (!pad) {
+    p0 = rep_ptr[n];
+    p1 = rep_ptr[n + 1];
+  } else {
+    p0 = rep_ptr[N] + (n - N) * 16;
+    p1 = min(rep_ptr[N + 1], p0 + 16);
+  }
+  if (p0 >= p1) return;
+  const int4 hr = pad ? make_int4(-1, -1, -1, -1) : hist[n];
+  if (blockIdx.x == 0 && threadIdx.x < HV) {  // per-head gates
+    const int h = threadIdx.x;
+    float bv = 0.f, gv = 0.f;
+    if (!pad) {
+      const uint16_t* row = proj + (int64_t)hr.w * P + C + VD;
+      bv = sigmoid_f(bf2f(row[h]));
+      const float xs = bf2f(row[HV + h]) + bf2f(dt_bias[h]);
+      gv = -expf(bf2f(A_log[h])) * (xs > 20.f ? xs : log1pf(expf(xs)));
+    }
+    const uint16_t bb = (uint16_t)f2bf(bv);
+    for (int p = p0; p < p1; ++p) {
+      const int64_t s = rep_pos[p];
+      beta[s * HV + h] = bb;
+      g[s * HV + h] = gv;
+    }
+  }
+  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
+  if (c0 >= C) return;  // C is a multiple of 128: a 16-lane head group is either all in or all out
+  uint4 ov = make_uint4(0u, 0u, 0u, 0u);
+  const bool isqk = c0 < 2 * KD;
+  if (!pad) {
+    const int rows[4] = {hr.x, hr.y, hr.z, hr.w};
+    uint4 xr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      xr[i] = rows[i] >= 0 ? *reinterpret_cast<const uint4*>(proj + (int64_t)rows[i] * P + c0) : make_uint4(0, 0, 0, 0);
+    uint4 wr[4];  // convw[c0 .. c0+8)[0..4): 64 contiguous bytes
+#pragma unroll
+    for (int u = 0; u < 4; ++u) wr[u] = *reinterpret_cast<const uint4*>(convw + (int64_t)c0 * 4 + u * 8);
+    const uint32_t* xw[4] = {&xr[0].x, &xr[1].x, &xr[2].x, &xr[3].x};
+    const uint32_t* ww = &wr[0].x;
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float acc = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t xb = (xw[i][j >> 1] >> ((j & 1) * 16)) & 0xffffu;
+        const uint32_t wb = (ww[(j * 4 + i) >> 1] >> (((j * 4 + i) & 1) * 16)) & 0xffffu;
+        acc += bf2f(wb) * bf2f(xb);
+      }
+      o[j] = rbf(silu_f(acc));
+    }
+    if (isqk) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) ss += o[j] * o[j];
+#pragma unroll
+      for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+      const float rs = 1.0f / sqrtf(ss + 1e-6f);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = o[j] * rs;
+    }
+    ov = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+  }
+  if (isqk) {
+    uint16_t* dst = c0 < KD ? q : k;
+    const int cc = c0 < KD ? c0 : c0 - KD;
+    const int hk = cc / HD, dd = cc - hk * HD;
+    const int64_t rowlen = (int64_t)RQ * KD;
+    for (int p = p0; p < p1; ++p) {
+      uint16_t* o = dst + (int64_t)rep_pos[p] * rowlen + (int64_t)hk * RQ * HD + dd;
+#pragma unroll
+      for (int r = 0; r < RQ; ++r) *reinterpret_cast<uint4*>(o + r * HD) = ov;
+    }
+  } else {
+    for (int p = p0; p < p1; ++p) *reinterpret_cast<uint4*>(v + (int64_t)rep_pos[p] * VD + (c0 - 2 * KD)) = ov;
+  }
+}
+
+hipError_t launch_linattn_prep(const uint16_t* proj, const int32_t* hist, const int32_t* rep_ptr,
+                               const int32_t* rep_pos, int64_t N, int64_t R, const uint16_t* convw,
+                               const uint16_t* A_log, const uint16_t* dt_bias, int KD, int VD, int HV, int RQ,
+                               uint16_t* q, uint16_t* k, uint16_t* v, float* g, uint16_t* beta, hipStream_t st) {
+  const int C = 2 * KD + VD;
+  const dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)(N + (R + 15) / 16));
+  if (RQ == 3)
+    hipLaunchKernelGGL(linattn_prep_k<3>, grid, dim3(256), 0, st, proj, reinterpret_cast<const int4*>(hist), rep_ptr,
+                       rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
+  else
+    hipLaunchKernelGGL(linattn_prep_k<1>, grid, dim3(256), 0, st, proj, reinterpret_cast<const int4*>(hist), rep_ptr,
+                       rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
+  return hipGetLastError();
+}
+
 }  // namespace ojx

@@ -351,6 +351,36 @@ def fullattn_prep2(proj, qw1, kw1, cos, sin, B, T, HQ, HKV, D, eps):
     return [qt.unsqueeze(0), kt.unsqueeze(0), vt.unsqueeze(0), gate]
 
 
+def linattn_prep_dedup2(proj, hist, rep_ptr, rep_pos, L2, convw, A_log, dt_bias, KD, VD, HV, HK, HD, rep_qk):
+    """The reference extension's linattn_prep_dedup2 (src/kernels.cu:1176-1290), as forward_gtree calls it
+    (src/fastmodel.py:420,438): [q [R, RQ KD], k, v [R, VD], g fp32 [R, HV], beta [R, HV]], R = rep_pos.numel(),
+    RQ = HV / HK when rep_qk else 1."""
+    _chk(proj, "proj", torch.bfloat16)
+    for t, nm in ((hist, "hist"), (rep_ptr, "rep_ptr"), (rep_pos, "rep_pos")):
+        _chk(t, nm, torch.int32)
+    for t, nm in ((convw, "convw"), (A_log, "A_log"), (dt_bias, "dt_bias")):
+        _chk(t, nm, torch.bfloat16)
+    N, R = proj.shape[0], rep_pos.numel()
+    C = 2 * KD + VD
+    if proj.dim() != 2 or proj.shape[1] != C + VD + 2 * HV:
+        raise RuntimeError(f"proj {tuple(proj.shape)} is not [N, 2 KD + 2 VD + 2 HV] for KD={KD} VD={VD} HV={HV}")
+    if convw.numel() != C * 4 or (convw.dim() == 2 and convw.shape[1] != 4):
+        raise RuntimeError(f"convw {tuple(convw.shape)} is not [{C}, 4]")
+    if hist.numel() != (N + 1) * 4 or rep_ptr.numel() != N + 2 or A_log.numel() != HV or dt_bias.numel() != HV:
+        raise RuntimeError("hist must be [N + 1, 4], rep_ptr [N + 2], A_log and dt_bias [HV]")
+    rq = HV // HK if rep_qk else 1
+    dev = proj.device
+    q = torch.empty((R, rq * KD), dtype=torch.bfloat16, device=dev)
+    k = torch.empty((R, rq * KD), dtype=torch.bfloat16, device=dev)
+    v = torch.empty((R, VD), dtype=torch.bfloat16, device=dev)
+    g = torch.empty((R, HV), dtype=torch.float32, device=dev)
+    beta = torch.empty((R, HV), dtype=torch.bfloat16, device=dev)
+    check(lib().ojx_linattn_prep(_ptr(proj), _ptr(hist), _ptr(rep_ptr), _ptr(rep_pos), N, R, int(L2), _ptr(convw),
+                                 _ptr(A_log), _ptr(dt_bias), KD, VD, HV, HK, HD, int(bool(rep_qk)), _ptr(q), _ptr(k),
+                                 _ptr(v), _ptr(g), _ptr(beta), _stream()))
+    return [q, k, v, g, beta]
+
+
 def mm_fullattn_prep(x, w_qkv, qw1, kw1, cos, sin, HQ, HKV, D, eps):
     """_mm(hn, d.w_in) + fullattn_prep2 in one kernel (src/fastmodel.py:412,462): the QKV in-projection with the
     prep in its epilogue. w_qkv row-major [(2 HQ + 2 HKV) D, K] or packed (pack_weight). Returns the prep's outputs

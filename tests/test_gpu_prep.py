@@ -116,3 +116,83 @@ def test_gemm_qkv_fullattn_prep_rejects(ext, dev):
         ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, 2, 1, 256, EPS)
     with pytest.raises(RuntimeError):  # weight rows do not match the head counts
         ext.mm_fullattn_prep(x, w[:512].contiguous(), qw1, kw1, cos, sin, 2, 1, 256, EPS)
+
+
+# ---------------------------------------------------------------- linear-attention prep (tree layout)
+def _lin_inputs(tree, HK, HV, seed, HD=128, NB=32, PB=16):
+    from oracle import linattn_oracle as LO
+    lay = LO.tree_layout(*tree, NB=NB, PB=PB)
+    KD, VD = HK * HD, HV * HD
+    C = 2 * KD + VD
+    g = torch.Generator().manual_seed(seed)
+    proj = (torch.randn(lay["N"], C + VD + 2 * HV, generator=g) * 1.5).bfloat16()
+    convw = (torch.randn(C, 4, generator=g) * 0.5).bfloat16()
+    A_log = torch.randn(HV, generator=g).bfloat16()
+    dt_bias = (torch.randn(HV, generator=g) * 4).bfloat16()
+    return LO, lay, proj, convw, A_log, dt_bias, KD, VD
+
+
+def _ulp_close(got, want, what, min_equal=0.99, steps=1):
+    """Equal almost everywhere; elsewhere within `steps` bf16 rounding steps. The device expf and numpy's may differ
+    in the last fp32 bit, which moves a SiLU output across a bf16 rounding boundary now and then (one step); a q / k
+    value is rounded once more after the head norm (two steps)."""
+    g, w = got.float().cpu(), want.float().cpu()
+    err = (g - w).abs()
+    lim = w.abs() * 2.0 ** -8 * (2 * steps)
+    assert bool((err <= lim).all()), f"{what}: {(err - lim).max():.3e}"
+    frac = (err == 0).float().mean().item()
+    assert frac >= min_equal, f"{what}: only {frac:.4f} equal"
+
+
+# (Lr, q_len, groups, l_len): the north star's lin-attn in-projection rows are ~288 packed tokens (a shared prompt,
+# group continuations, candidate leaves); one tree with no padding slots at all, one with rows that no slot holds.
+_TREES = {
+    "m288": (200, [20, 12, 9], [0, 0, 1, 1, 2, 2, 0, 1], [5, 7, 3, 6, 2, 4, 1, 3]),
+    "nopad": (10, [2], [0, 0], [4, 4]),
+    "tiny": (1, [0], [0], [1]),   # two real rows on one path
+}
+
+
+@pytest.mark.parametrize("tree", list(_TREES))
+@pytest.mark.parametrize("rep_qk", [False, True])
+def test_linattn_prep_vs_oracle(ext, dev, tree, rep_qk):
+    HK, HV, HD = 16, 48, 128   # Qwen3.5 linear attention: KD 2048, VD 6144, proj width 16480
+    if tree == "tiny":
+        HK, HV = 1, 3
+    t = _TREES[tree]
+    _say(f"case linattn_prep tree={tree} rep_qk={rep_qk}")
+    LO, lay, proj, convw, A_log, dt_bias, KD, VD = _lin_inputs(t, HK, HV, seed=len(tree), PB=8 if tree == "nopad"
+                                                               else 16)
+    if tree == "nopad":
+        assert lay["rep_ptr"][lay["N"]] == lay["rep_ptr"][lay["N"] + 1]   # no end-padding slot
+    d = lambda a: torch.as_tensor(a).to(dev).contiguous()  # noqa: E731
+    q, k, v, g, beta = ext.linattn_prep_dedup2(proj.to(dev), d(lay["hist"]), d(lay["rep_ptr"]), d(lay["rep_pos"]),
+                                               lay["L2"], convw.to(dev), A_log.to(dev), dt_bias.to(dev), KD, VD, HV,
+                                               HK, 128, rep_qk)
+    torch.cuda.synchronize()
+    rq_, rk_, rv_, rg_, rb_ = LO.linattn_prep(proj, lay["hist"], lay["rep_ptr"], lay["rep_pos"], lay["L2"], convw,
+                                              A_log, dt_bias, KD, VD, HV, HK, 128, rep_qk)
+    assert q.shape == rq_.shape and v.shape == rv_.shape and g.dtype == torch.float32
+    _ulp_close(v, rv_, "v")
+    _ulp_close(q, rq_, "q", steps=2)
+    _ulp_close(k, rk_, "k", steps=2)
+    _ulp_close(beta, rb_, "beta")
+    assert torch.allclose(g.cpu(), rg_, rtol=2e-6, atol=0), (g.cpu() - rg_).abs().max()
+    pad = torch.as_tensor(lay["src"].reshape(-1) < 0)
+    for tnsr in (q, k, v, g, beta):   # padding slots are written (zeros), not left as they were
+        assert bool((tnsr.cpu()[pad] == 0).all())
+
+
+def test_linattn_prep_rejects(ext, dev):
+    LO, lay, proj, convw, A_log, dt_bias, KD, VD = _lin_inputs(_TREES["nopad"], 2, 6, seed=1)
+    d = lambda a: torch.as_tensor(a).to(dev).contiguous()  # noqa: E731
+    args = [proj.to(dev), d(lay["hist"]), d(lay["rep_ptr"]), d(lay["rep_pos"]), lay["L2"], convw.to(dev),
+            A_log.to(dev), dt_bias.to(dev), KD, VD, 6, 2]
+    with pytest.raises(RuntimeError):
+        ext.linattn_prep_dedup2(*args, 64, False)           # head_dim 64
+    with pytest.raises(RuntimeError):
+        ext.linattn_prep_dedup2(*args[:4], lay["L2"] + 1, *args[5:], 128, False)   # R not a multiple of L2
+    with pytest.raises(RuntimeError):                       # rep_qk with HV / HK = 3 only
+        a2 = list(args)
+        a2[10] = 8
+        ext.linattn_prep_dedup2(*a2, 128, True)

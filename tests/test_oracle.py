@@ -296,3 +296,83 @@ def test_fullattn_prep_rotation_and_copies_exact():
     c = torch.full((1, P), 2.0).bfloat16()
     qc, kc, _, _ = O.fullattn_prep(c, torch.ones(D), torch.ones(D), one[:1], zero[:1], HQ, HKV, D, 0.0)
     assert bool((qc == 1.0).all()) and bool((kc == 1.0).all())
+
+
+# ---------------------------------------------------------------- linear-attention prep (tree layout)
+
+def _lin_case(seed, HK=2, HV=6, HD=128, Lr=5, q_len=(3, 0, 4), groups=(0, 0, 1, 2, 1), l_len=(2, 6, 1, 3, 4)):
+    from oracle import linattn_oracle as LO
+    lay = LO.tree_layout(Lr, list(q_len), list(groups), list(l_len), NB=16, PB=8)
+    KD, VD = HK * HD, HV * HD
+    C = 2 * KD + VD
+    g = torch.Generator().manual_seed(seed)
+    proj = (torch.randn(lay["N"], C + VD + 2 * HV, generator=g) * 1.5).bfloat16()
+    convw = (torch.randn(C, 4, generator=g) * 0.5).bfloat16()
+    A_log = torch.randn(HV, generator=g).bfloat16()
+    dt_bias = (torch.randn(HV, generator=g) * 4).bfloat16()
+    return LO, lay, proj, convw, A_log, dt_bias, KD, VD, HV, HK, HD
+
+
+def test_tree_layout_vs_walk():
+    """rep_ptr / rep_pos list, for every packed row, exactly the slots holding it (ascending slot order, padding
+    last), and hist[n] is the 4-row window ending at n on any path through n."""
+    from oracle import linattn_oracle as LO
+    lay = LO.tree_layout(4, [2, 5], [1, 0, 1], [3, 1, 2], NB=16, PB=8)
+    N, S, L2, src = lay["N"], lay["S"], lay["L2"], lay["src"]
+    assert N % 16 == 0 and L2 % 8 == 0 and src.shape == (S, L2)
+    flat = src.reshape(-1)
+    for n in range(N + 1):
+        got = lay["rep_pos"][lay["rep_ptr"][n]:lay["rep_ptr"][n + 1]].tolist()
+        want = [s for s in range(S * L2) if (flat[s] == n if n < N else flat[s] < 0)]
+        assert got == want, n
+        for s in want if n < N else []:
+            c, t = divmod(s, L2)
+            assert [src[c, t - 3 + i] if t - 3 + i >= 0 else -1 for i in range(4)] == lay["hist"][n].tolist()
+    assert (lay["hist"][N] == -1).all()
+    # the root is shared by all paths; a leaf row by exactly one
+    assert lay["rep_ptr"][1] - lay["rep_ptr"][0] == S
+
+
+@pytest.mark.parametrize("rep_qk", [False, True])
+def test_linattn_prep_vs_slot_f64(rep_qk):
+    LO, lay, proj, convw, A_log, dt_bias, KD, VD, HV, HK, HD = _lin_case(3)
+    q, k, v, gg, beta = LO.linattn_prep(proj, lay["hist"], lay["rep_ptr"], lay["rep_pos"], lay["L2"], convw, A_log,
+                                        dt_bias, KD, VD, HV, HK, HD, rep_qk)
+    qk64, v64, g64, b64 = LO.linattn_slot_f64(proj, lay["src"], convw, A_log, dt_bias, KD, VD, HV, HD)
+    rq = HV // HK if rep_qk else 1
+    R = lay["S"] * lay["L2"]
+    assert q.shape == (R, rq * KD) and v.shape == (R, VD) and gg.dtype == torch.float32
+    qf = q.float().numpy().reshape(R, KD // HD, rq, HD)
+    kf = k.float().numpy().reshape(R, KD // HD, rq, HD)
+    for r in range(1, rq):  # replicated heads are copies
+        assert (qf[:, :, r] == qf[:, :, 0]).all() and (kf[:, :, r] == kf[:, :, 0]).all()
+    got_qk = np.concatenate([qf[:, :, 0].reshape(R, KD), kf[:, :, 0].reshape(R, KD)], 1)
+    # q / k: unit-norm heads, two bf16 roundings (silu output, normalised value): 2^-7 of the value + 2^-9
+    assert (np.abs(got_qk - qk64) <= np.abs(qk64) * 2.0 ** -7 + 2.0 ** -9).all()
+    # v: one bf16 rounding of silu(conv)
+    vf = v.float().numpy()
+    assert (np.abs(vf - v64) <= np.abs(v64) * 2.0 ** -8 + 1e-6).all()
+    assert np.allclose(gg.numpy(), g64, rtol=1e-5, atol=1e-6)
+    assert (np.abs(beta.float().numpy() - b64) <= b64 * 2.0 ** -8).all()
+    pad = lay["src"].reshape(-1) < 0
+    assert pad.any() and (got_qk[pad] == 0).all() and (vf[pad] == 0).all() and (gg.numpy()[pad] == 0).all()
+    # every real slot's q / k head has unit norm (up to bf16 rounding)
+    nrm = np.sqrt((got_qk[~pad].reshape(-1, HD) ** 2).sum(1))
+    assert np.abs(nrm - 1).max() < 2e-2
+
+
+def test_linattn_gates_closed_forms():
+    """beta against scipy's expit, g against -exp(A_log) * log(1 + e^x) (numpy logaddexp), including the
+    softplus branch above 20 and very negative arguments."""
+    from scipy.special import expit
+    from oracle import linattn_oracle as LO
+    b = np.array([-30, -5, -0.5, 0, 0.25, 3, 30], np.float32)
+    a = np.array([-40, -3, 0, 1, 19.5, 20.5, 60], np.float32)
+    al = np.array([0.5] * 7, np.float32)
+    db = np.zeros(7, np.float32)
+    beta, g = LO._gates(b, a, al, db)
+    want_b = expit(b.astype(np.float64))
+    assert (np.abs(beta - want_b) <= want_b * 2.0 ** -8).all()
+    want_g = -np.exp(0.5) * np.logaddexp(0.0, a.astype(np.float64))
+    assert np.allclose(g, want_g, rtol=2e-6, atol=1e-30)
+    assert g[-1] == np.float32(-np.exp(np.float32(0.5)) * np.float32(60))  # x > 20: softplus(x) = x exactly
