@@ -143,7 +143,7 @@ int ojx_gemm_residual_rmsnorm_pk(const void* x, const void* wp, const void* resi
  * forward_gtree, src/fastmodel.py:462). proj [N, (2 HQ + 2 HKV) D] bf16 (per q head: D q dims then D gate dims; then
  * the k heads, then the v heads). q and k heads: RMSNorm over the head (weight qw1 / kw1 fp32 [D], eps), then the
  * rotate-half RoPE on the first RD dims with cos / sin bf16 [N, RD]; outputs qt [HQ, N, D], kt [HKV, N, D],
- * vt [HKV, N, D] (v copied) and gate [N, HQ D] (copied), all bf16. D = 256; RD = 8 * a power of two, <= D. */
+ * vt [HKV, N, D] (v copied) and gate [N, HQ D] (copied), all bf16. D = 256; RD = 16 * a power of two, <= D. */
 int ojx_fullattn_prep(const void* proj, int64_t N, int32_t HQ, int32_t HKV, int32_t D, int32_t RD, float eps,
                       const float* qw1, const float* kw1, const void* cosb, const void* sinb, void* qt, void* kt,
                       void* vt, void* gate, ojx_stream_t stream);

@@ -11,23 +11,27 @@
 //   Outputs (B = 1, T = N): qt [HQ, N, D], kt [HKV, N, D], vt [HKV, N, D] (head-major for attention) and
 //   gate [N, HQ D].
 //
-// One wave64 per (token, head task), 4 consecutive dims per lane (D = 256): the row's sum of squares is a wave
-// butterfly, and the RoPE partner of lane l is lane l ^ (RD / 8), because dims d and d +- RD/2 sit RD/8 lanes
-// apart and RD/8 is a power of two below 16 (RD in {32, 64, 128}).
+// Two (token, head task) pairs per wave64, 32 lanes each with 8 consecutive dims (one 16-byte load and store per
+// lane, D = 256): the row's sum of squares is a butterfly over the 32 lanes, and the RoPE partner of lane l is lane
+// l ^ (RD / 16), because dims d and d +- RD/2 sit RD/16 lanes apart and RD/16 is a power of two below 32
+// (RD = 16 .. 256).
 #include "ojx_internal.h"
 
 namespace ojx {
 
 namespace {
 
-__device__ __forceinline__ void unpack4(uint2 a, float (&v)[4]) {
-  v[0] = bf2f(a.x & 0xffffu); v[1] = bf2f(a.x >> 16); v[2] = bf2f(a.y & 0xffffu); v[3] = bf2f(a.y >> 16);
+__device__ __forceinline__ void unpack8(uint4 a, float (&v)[8]) {
+  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf2f(w[i] & 0xffffu);
+    v[2 * i + 1] = bf2f(w[i] >> 16);
+  }
 }
-__device__ __forceinline__ uint2 pack4(const float (&v)[4]) { return make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3])); }
 
 }  // namespace
 
-// FD: dims per lane (D / 64)
 __global__ void __launch_bounds__(256) fullattn_prep_k(const uint16_t* __restrict__ proj, int64_t N, int HQ, int HKV,
                                                        int RD, float eps, const float* __restrict__ qw1,
                                                        const float* __restrict__ kw1, const uint16_t* __restrict__ cosb,
@@ -35,62 +39,66 @@ __global__ void __launch_bounds__(256) fullattn_prep_k(const uint16_t* __restric
                                                        uint16_t* __restrict__ kt, uint16_t* __restrict__ vt,
                                                        uint16_t* __restrict__ gate) {
   constexpr int D = 256;
-  const int lane = threadIdx.x & 63;
+  const int lane = threadIdx.x & 31;
   const int ntask = HQ + 2 * HKV;
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (wid >= N * ntask) return;
+  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
+  if (wid >= N * ntask) return;  // whole 32-lane halves leave together
   const int64_t n = wid / ntask;
   const int task = (int)(wid - n * ntask);
   const int64_t P = (int64_t)(2 * HQ + 2 * HKV) * D;
   const uint16_t* row = proj + n * P;
-  const int d0 = lane * 4;
+  const int d0 = lane * 8;
   if (task >= HQ + HKV) {  // v head: a copy into [HKV, N, D]
     const int h = task - HQ - HKV;
-    *reinterpret_cast<uint2*>(vt + ((int64_t)h * N + n) * D + d0) =
-        *reinterpret_cast<const uint2*>(row + 2 * HQ * D + HKV * D + h * D + d0);
+    *reinterpret_cast<uint4*>(vt + ((int64_t)h * N + n) * D + d0) =
+        *reinterpret_cast<const uint4*>(row + 2 * HQ * D + HKV * D + h * D + d0);
     return;
   }
   const bool isq = task < HQ;
   const int h = isq ? task : task - HQ;
   if (isq)  // gate head: a copy into [N, HQ D]
-    *reinterpret_cast<uint2*>(gate + n * (int64_t)(HQ * D) + h * D + d0) =
-        *reinterpret_cast<const uint2*>(row + (int64_t)h * 2 * D + D + d0);
-  float x[4];
-  unpack4(*reinterpret_cast<const uint2*>(row + (isq ? (int64_t)h * 2 * D : 2 * HQ * D + (int64_t)h * D) + d0), x);
+    *reinterpret_cast<uint4*>(gate + n * (int64_t)(HQ * D) + h * D + d0) =
+        *reinterpret_cast<const uint4*>(row + (int64_t)h * 2 * D + D + d0);
+  float x[8];
+  unpack8(*reinterpret_cast<const uint4*>(row + (isq ? (int64_t)h * 2 * D : 2 * HQ * D + (int64_t)h * D) + d0), x);
   float ss = 0.f;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) ss += x[j] * x[j];
+  for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
 #pragma unroll
-  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
   const float r = rsqrtf(ss / (float)D + eps);
-  const float* w1 = isq ? qw1 : kw1;
-  const float4 wv = *reinterpret_cast<const float4*>(w1 + d0);
-  float nv[4] = {rbf((x[0] * r) * wv.x), rbf((x[1] * r) * wv.y), rbf((x[2] * r) * wv.z), rbf((x[3] * r) * wv.w)};
-  const int hl = RD >> 3;  // partner lane distance
-  float pv[4];
+  const float* w1 = (isq ? qw1 : kw1) + d0;
+  const float4 wa = *reinterpret_cast<const float4*>(w1), wb = *reinterpret_cast<const float4*>(w1 + 4);
+  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+  float nv[8];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) pv[j] = __shfl_xor(nv[j], hl);
-  float out[4];
+  for (int j = 0; j < 8; ++j) nv[j] = rbf((x[j] * r) * wv[j]);
+  const int hl = RD >> 4;  // partner lane distance
+  float pv[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) pv[j] = __shfl_xor(nv[j], hl);
+  float out[8];
   if (d0 < RD) {
-    float c[4], s[4];
-    unpack4(*reinterpret_cast<const uint2*>(cosb + n * RD + d0), c);
-    unpack4(*reinterpret_cast<const uint2*>(sinb + n * RD + d0), s);
+    float c[8], sn[8];
+    unpack8(*reinterpret_cast<const uint4*>(cosb + n * RD + d0), c);
+    unpack8(*reinterpret_cast<const uint4*>(sinb + n * RD + d0), sn);
     const bool lo = d0 < RD / 2;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = rbf(rbf(nv[j] * c[j]) + rbf((lo ? -pv[j] : pv[j]) * s[j]));
+    for (int j = 0; j < 8; ++j) out[j] = rbf(rbf(nv[j] * c[j]) + rbf((lo ? -pv[j] : pv[j]) * sn[j]));
   } else {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) out[j] = nv[j];
+    for (int j = 0; j < 8; ++j) out[j] = nv[j];
   }
   uint16_t* dst = isq ? qt : kt;
-  *reinterpret_cast<uint2*>(dst + ((int64_t)h * N + n) * D + d0) = pack4(out);
+  *reinterpret_cast<uint4*>(dst + ((int64_t)h * N + n) * D + d0) =
+      make_uint4(pack2(out[0], out[1]), pack2(out[2], out[3]), pack2(out[4], out[5]), pack2(out[6], out[7]));
 }
 
 hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV, int RD, float eps,
                                 const float* qw1, const float* kw1, const uint16_t* cosb, const uint16_t* sinb,
                                 uint16_t* qt, uint16_t* kt, uint16_t* vt, uint16_t* gate, hipStream_t st) {
-  const int64_t waves = N * (HQ + 2 * HKV);
-  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)((waves + 3) / 4)), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps,
+  const int64_t halves = N * (HQ + 2 * HKV);
+  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)((halves + 7) / 8)), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps,
                      qw1, kw1, cosb, sinb, qt, kt, vt, gate);
   return hipGetLastError();
 }
@@ -114,8 +122,8 @@ hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV
 //
 // Layout of the work: a workgroup of 256 lanes takes 2048 channels of one packed row (each lane 8 consecutive
 // channels, one 16-byte load per history row, 16 lanes = one q/k head), computes them once and stores them to each of
-// the row's slots (a wave writes 1 KB contiguous per slot). Workgroups with y >= N write the end-padding slots,
-// 16 slots each. Products of two bf16 values are exact in fp32, so the conv's sum is the only rounding order that
+// the row's slots (a wave writes 1 KB contiguous per slot). Workgroups past the N packed rows write the
+// end-padding slots, 16 slots each. Products of two bf16 values are exact in fp32, so the conv's sum is the only rounding order that
 // matters, and it is kept.
 template <int RQ>
 __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict__ proj, const int4* __restrict__ hist,
@@ -129,7 +137,9 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
   constexpr int HD = 128;
   const int C = 2 * KD + VD;
   const int64_t P = (int64_t)C + VD + 2 * HV;
-  const int n = blockIdx.y;
+  // plain row-major numbering: an XCD-contiguous run of rows was measured slower (the prompt rows, written to
+  // every path, then pile onto one XCD)
+  const int n = blockIdx.y, bx = blockIdx.x;
   const bool pad = n >= N;
   int p0, p1;
   if (!pad) {
@@ -141,27 +151,21 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
   }
   if (p0 >= p1) return;
   const int4 hr = pad ? make_int4(-1, -1, -1, -1) : hist[n];
-  if (blockIdx.x == 0 && threadIdx.x < HV) {  // per-head gates
-    const int h = threadIdx.x;
-    float bv = 0.f, gv = 0.f;
-    if (!pad) {
-      const uint16_t* row = proj + (int64_t)hr.w * P + C + VD;
-      bv = sigmoid_f(bf2f(row[h]));
-      const float xs = bf2f(row[HV + h]) + bf2f(dt_bias[h]);
-      gv = -expf(bf2f(A_log[h])) * (xs > 20.f ? xs : log1pf(expf(xs)));
-    }
-    const uint16_t bb = (uint16_t)f2bf(bv);
-    for (int p = p0; p < p1; ++p) {
-      const int64_t s = rep_pos[p];
-      beta[s * HV + h] = bb;
-      g[s * HV + h] = gv;
-    }
+  const int tid = threadIdx.x;
+  const bool gate_lane = bx == 0 && tid < HV;  // per-head gates
+  float bv = 0.f, gv = 0.f;
+  if (gate_lane && !pad) {
+    const uint16_t* row = proj + (int64_t)hr.w * P + C + VD;
+    bv = sigmoid_f(bf2f(row[tid]));
+    const float xs = bf2f(row[HV + tid]) + bf2f(dt_bias[tid]);
+    gv = -expf(bf2f(A_log[tid])) * (xs > 20.f ? xs : log1pf(expf(xs)));
   }
-  const int c0 = (blockIdx.x * 256 + threadIdx.x) * 8;
-  if (c0 >= C) return;  // C is a multiple of 128: a 16-lane head group is either all in or all out
-  uint4 ov = make_uint4(0u, 0u, 0u, 0u);
+  const uint16_t bb = (uint16_t)f2bf(bv);
+  const int c0 = (bx * 256 + tid) * 8;
+  const bool live = c0 < C;  // C is a multiple of 128: a 16-lane head group is either all in or all out
   const bool isqk = c0 < 2 * KD;
-  if (!pad) {
+  uint4 ov = make_uint4(0u, 0u, 0u, 0u);
+  if (live && !pad) {
     const int rows[4] = {hr.x, hr.y, hr.z, hr.w};
     uint4 xr[4];
 #pragma unroll
@@ -196,18 +200,38 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
     }
     ov = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
   }
+  // destination of this lane's 8 channels within a slot's row
+  uint16_t* dst;
+  int64_t rowlen;
   if (isqk) {
-    uint16_t* dst = c0 < KD ? q : k;
     const int cc = c0 < KD ? c0 : c0 - KD;
-    const int hk = cc / HD, dd = cc - hk * HD;
-    const int64_t rowlen = (int64_t)RQ * KD;
-    for (int p = p0; p < p1; ++p) {
-      uint16_t* o = dst + (int64_t)rep_pos[p] * rowlen + (int64_t)hk * RQ * HD + dd;
-#pragma unroll
-      for (int r = 0; r < RQ; ++r) *reinterpret_cast<uint4*>(o + r * HD) = ov;
-    }
+    const int hk = cc / HD;
+    dst = (c0 < KD ? q : k) + (int64_t)hk * RQ * HD + (cc - hk * HD);
+    rowlen = (int64_t)RQ * KD;
   } else {
-    for (int p = p0; p < p1; ++p) *reinterpret_cast<uint4*>(v + (int64_t)rep_pos[p] * VD + (c0 - 2 * KD)) = ov;
+    dst = v + (c0 - 2 * KD);
+    rowlen = VD;
+  }
+  // The row's slots, staged through LDS 256 at a time: one coalesced load, then every lane reads the slot ids as
+  // LDS broadcasts (independent reads the compiler can issue ahead, instead of a chain of dependent scalar loads).
+  __shared__ int slot[256];
+  for (int base = p0; base < p1; base += 256) {
+    const int cnt = min(256, p1 - base);
+    if (tid < cnt) slot[tid] = rep_pos[base + tid];
+    __syncthreads();
+    if (gate_lane)
+      for (int j = 0; j < cnt; ++j) {
+        const int64_t sp = slot[j];
+        beta[sp * HV + tid] = bb;
+        g[sp * HV + tid] = gv;
+      }
+    if (live)
+      for (int j = 0; j < cnt; ++j) {
+        uint16_t* o = dst + (int64_t)slot[j] * rowlen;
+#pragma unroll
+        for (int r = 0; r < (isqk ? RQ : 1); ++r) *reinterpret_cast<uint4*>(o + r * HD) = ov;
+      }
+    __syncthreads();
   }
 }
 
