@@ -75,6 +75,15 @@ __device__ __forceinline__ void dma16_nt(__amdgpu_buffer_rsrc_t r, void* lds, ui
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, 0, 0, 2);
 }
 
+// The LDS DMA with a wave-uniform byte offset (soffset) added to the lane's offset: loop-invariant lane offsets in
+// VGPRs, the per-stage part in an SGPR, so that issuing a DMA costs no vector instruction.
+__device__ __forceinline__ void dma16s(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 0);
+}
+__device__ __forceinline__ void dma16s_nt(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds, 16, voff, soff, 0, 2);
+}
+
 // Workgroup barrier that orders LDS only. __syncthreads() is a full workgroup fence, which on gfx9 waits for every
 // outstanding global load (vmcnt(0)) and would drain the weight prefetch queue at each x-tile handoff.
 __device__ __forceinline__ void lds_barrier() {

@@ -151,7 +151,7 @@ __device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&a
 
 // REV (two leftover x fragments only): the group walks its W fragments from the last one down, so that its extra
 // fragments (the upper half) come first; the other groups walk upwards. Either way the walk is static code.
-template <int FW, int FX, int XE, int EPI, bool REV>
+template <int FW, int FX, int XE, int EPI, bool REV, bool PK>
 __device__ __forceinline__ void kx_body(const GemmParams& p) {
   using S = KxShape<FW, FX, XE>;
   constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW, GPW = S::GPW;
@@ -179,7 +179,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   const int nk = ke > kb ? (ke - kb + BK - 1) / BK : 0;
 
   // row-major W: this tile's rows only (rows past N read zeros); packed W: the whole buffer, blocks past N skipped
-  const __amdgpu_buffer_rsrc_t rsW = p.wpk ? make_rsrc(p.W, (int64_t)p.N * p.K * 2)
+  const __amdgpu_buffer_rsrc_t rsW = PK ? make_rsrc(p.W, (int64_t)p.N * p.K * 2)
                                            : make_rsrc(p.W + (int64_t)n0 * p.ldw, (int64_t)min(BN, p.N - n0) * p.ldw * 2);
   const int nbw = p.N >> 4;  // 16-row blocks of the packed W
   const __amdgpu_buffer_rsrc_t rsX = make_rsrc(p.X + (int64_t)m0 * p.ldx, (int64_t)min(BM, p.M - m0) * p.ldx * 2);
@@ -216,43 +216,70 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   uint8_t* const wring = smem;
   uint8_t* const xring = smem + S::WD * WST;
   constexpr int XB = BM / 8, WB = BN / 8, NB = XB + WB;
-  // Batch block c = wave + 8 i (i < GPW): x block c if c < XB, else W block c - XB; waves past the end repeat the
-  // last block (same bytes to the same place), so every wave issues GPW DMAs per batch. Per-lane parts of the
-  // offsets for an even and an odd block (the swizzle depends on the block's parity); the block's own part is
-  // wave-uniform and computed at issue.
-  int kcp[2];
-  uint32_t lx[2], lw[2], lpk[2];
+  // Batch slot i (i < GPW) of a wave fetches block c = wave + 8 i of a stage: x block c if c < XB, else W block
+  // c - XB; waves past the end repeat the last block (same bytes to the same place), so every wave issues GPW DMAs
+  // per batch. Only the stage changes from batch to batch: each slot's lane offset at stage 0 is computed once
+  // (a VGPR per slot), and the stage's byte offset is a wave-uniform SGPR passed as the DMA's soffset. A stage past
+  // the end reads through an empty descriptor (zeros). Slots whose kind (x or W) is the same for every wave are
+  // told apart at compile time; at most one slot is x for some waves and W for others.
+  uint32_t voff[GPW], lblk[GPW];
+  bool isw_[GPW];
 #pragma unroll
-  for (int par = 0; par < 2; ++par) {
-    kcp[par] = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;
-    lx[par] = (uint32_t)(((lane >> 3) * p.ldx + kcp[par]) * 2);
-    lw[par] = (uint32_t)(((lane >> 3) * p.ldw + kcp[par]) * 2);
-    lpk[par] = (uint32_t)(((lane >> 3) * 64 + kcp[par]) * 2);  // packed: rows of 128 bytes
+  for (int i = 0; i < GPW; ++i) {
+    const int c = min(wave + i * NW, NB - 1);  // wave-uniform
+    const bool isw = c >= XB;
+    const int blk = isw ? c - XB : c, par = blk & 1;
+    const int kc = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;  // the chunk's 16-byte swizzle
+    uint32_t o;
+    if (isw) {
+      if constexpr (PK) {  // stage 0, row block (n0 + 8 blk) / 16, rows (8 blk) % 16 .. +7: 1 KiB contiguous
+        const int row = ((n0 >> 4) + (blk >> 1)) * 16 + (blk & 1) * 8 + (lane >> 3);
+        o = n0 + blk * 8 < p.N ? (uint32_t)((row * 64 + kc) * 2) : kOOB;
+      }
+      else
+        o = (uint32_t)(((int64_t)(blk * 8 + (lane >> 3)) * p.ldw + kb + kc) * 2);
+    } else {
+      o = (uint32_t)(((int64_t)(blk * 8 + (lane >> 3)) * p.ldx + kb + kc) * 2);
+    }
+    voff[i] = o;
+    lblk[i] = (uint32_t)(blk * 1024);
+    isw_[i] = isw;
+  }
+  const __amdgpu_buffer_rsrc_t rsNone = make_rsrc(p.W, 0);
+  // A split whose K range is not a multiple of 64 ends in a partial stage, where lanes past ke read zeros: bit i of
+  // tmask says whether this lane's slot i is inside the range at that stage (computed once, outside the loop).
+  const bool ragged = ((ke - kb) & (BK - 1)) != 0;
+  uint32_t tmask = 0;
+#pragma unroll
+  for (int i = 0; i < GPW; ++i) {
+    const int par = (int)(lblk[i] >> 10) & 1;
+    const int kc = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;
+    tmask |= (kb + (nk - 1) * BK + kc < ke ? 1u : 0u) << i;
   }
   // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
   auto dma = [&](int st, int lo, int hi) {
-    const int k0 = kb + st * BK;
+    const bool ok = st < nk;
+    const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in voff
+    const uint32_t sw = PK ? (uint32_t)(((kb >> 6) + st) * nbw * 2048) : sx;
+    const __amdgpu_buffer_rsrc_t rX = ok ? rsX : rsNone, rW = ok ? rsW : rsNone;
+    uint8_t* const xd = xring + (st & 1) * XST;
+    uint8_t* const wd = wring + (st % S::WD) * WST;
+    auto issue = [&](int i, uint32_t vo) {
+      const bool allx = NW * i + NW - 1 < XB, allw = NW * i >= XB;  // compile-time after unrolling
+      if (allx || (!allw && !isw_[i])) dma16s(rX, xd + lblk[i], vo, sx);
+      else dma16s_nt(rW, wd + lblk[i], vo, sw);
+    };
+    if (ragged && st == nk - 1) {  // rare
 #pragma unroll
-    for (int i = 0; i < GPW; ++i) {
-      if (i < lo || i >= hi) continue;
-      const int c = min(wave + i * NW, NB - 1);  // wave-uniform
-      const bool isw = c >= XB;
-      const int blk = isw ? c - XB : c, par = blk & 1;
-      const bool ok = st < nk && k0 + kcp[par] < ke;
-      if (isw) {
-        uint32_t o;
-        bool okw = ok;
-        if (p.wpk) {
-          // stage k0 / 64, row block (n0 + 8 blk) / 16, rows (8 blk) % 16 .. +7: 1 KiB contiguous
-          o = (uint32_t)((((k0 >> 6) * nbw + ((n0 >> 4) + (blk >> 1))) * 16 + (blk & 1) * 8) * 128) + lpk[par];
-          okw = ok && n0 + blk * 8 < p.N;
-        } else {
-          o = (uint32_t)(blk * 8 * p.ldw * 2) + lw[par] + (uint32_t)k0 * 2u;
-        }
-        dma16_nt(rsW, wring + (st % S::WD) * WST + blk * 1024, okw ? o : kOOB);
-      } else {
-        const uint32_t o = (uint32_t)(blk * 8 * p.ldx * 2) + lx[par] + (uint32_t)k0 * 2u;
-        dma16(rsX, xring + (st & 1) * XST + blk * 1024, ok ? o : kOOB);
+      for (int i = 0; i < GPW; ++i) {
+        if (i < lo || i >= hi) continue;
+        issue(i, (tmask >> i) & 1u ? voff[i] : kOOB);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < GPW; ++i) {
+        if (i < lo || i >= hi) continue;
+        issue(i, voff[i]);
       }
     }
   };
@@ -395,8 +422,13 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
 template <int FW, int FX, int XE, int EPI>
 __device__ __forceinline__ void kx_dir(const GemmParams& p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true>(p);
-  else kx_body<FW, FX, XE, EPI, false>(p);
+  if (p.wpk) {
+    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true, true>(p);
+    else kx_body<FW, FX, XE, EPI, false, true>(p);
+  } else {
+    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true, false>(p);
+    else kx_body<FW, FX, XE, EPI, false, false>(p);
+  }
 }
 
 template <int FW, int FX, int XE>
