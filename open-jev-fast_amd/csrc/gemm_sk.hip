@@ -72,7 +72,7 @@ __device__ __forceinline__ void sk_sched() {  // NGA = groups before the barrier
 
 namespace {
 // The kernel body, specialised per epilogue mode (EPI) so that the epilogue is straight code for one mode.
-template <int FN, int FM, int WN, int WM, int EPI>
+template <int FN, int FM, int WN, int WM, int EPI, bool PK>
 __device__ __forceinline__ void sk_body(const GemmParams& p) {
   constexpr int BN = WN * FN * 16, BM = WM * FM * 16;
   constexpr int BK = 64, ROWS = BN + BM;
@@ -96,7 +96,6 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
   const int tiles_m = p.tiles_m;
   const int64_t ldw = p.ldw, ldx = p.ldx;
   const uint16_t* const Wp = p.W;
-  const bool wpk = p.wpk != 0;  // W in the packed layout
   const int nbw = N >> 4;       // its 16-row blocks
   const uint16_t* const Xp = p.X;
 
@@ -158,9 +157,10 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     // descriptors cover this tile's rows only: rows past N (or M) read zeros. A packed W (stage-major
     // [K/64][N/16][16][64], see ojx_pack_weight) is addressed through one descriptor over the whole buffer: W block
     // blk of a stage is 1 KiB at row block n0/16 + blk/2, half blk & 1, and blocks past N are skipped.
-    const __amdgpu_buffer_rsrc_t rsW = wpk ? make_rsrc(Wp, (int64_t)N * K * 2)
+    const __amdgpu_buffer_rsrc_t rsW = PK ? make_rsrc(Wp, (int64_t)N * K * 2)
                                            : make_rsrc(Wp + (int64_t)n0 * ldw, (int64_t)min(BN, N - n0) * ldw * 2);
     const __amdgpu_buffer_rsrc_t rsX = make_rsrc(Xp + (int64_t)m0 * ldx, (int64_t)min(BM, M - m0) * ldx * 2);
+    const __amdgpu_buffer_rsrc_t rsNone = make_rsrc(Wp, 0);
     const uint32_t dWp0 = (uint32_t)((((n0 >> 4) + (wave >> 1)) * 16 + (wave & 1) * 8 + (lane >> 3)) * 128 + kcol * 2);
 
 #pragma unroll
@@ -169,22 +169,34 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       for (int j = 0; j < FM; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     // ------------------------------------------------------------------ main loop
+    // DMAs lo .. hi-1 of the stage at k0 into buffer buf. The k offset (and, packed, the stage and block offset) is
+    // wave-uniform and goes in the DMA's soffset; only the row-major block offset costs a vector add. A stage past
+    // the segment reads zeros through an empty descriptor, W blocks past N (packed) likewise; only a partial last
+    // stage (a K range that is not a multiple of 64) needs per-lane checks, on a separate path.
 #define OJX_SK_DMA(buf, k0, lo, hi)                                                                        \
   do {                                                                                                     \
-    const uint32_t kof_ = (uint32_t)(k0) * 2u;                                                             \
+    const int k0_ = (k0);                                                                                  \
+    const bool live_ = k0_ < ke;                                                                           \
+    const bool part_ = live_ && k0_ + BK > ke;                                                             \
+    const uint32_t sk_ = (uint32_t)k0_ * 2u;                                                               \
+    const uint32_t skp_ = (uint32_t)(k0_ >> 6) * (uint32_t)nbw * 2048u;                                    \
+    const __amdgpu_buffer_rsrc_t rX_ = live_ ? rsX : rsNone, rW_ = live_ ? rsW : rsNone;                   \
     /* keep the per-block offsets as one multiply-add each instead of GPW registers held across the loop */ \
     asm volatile("" : "+s"(stepW), "+s"(stepX));                                                           \
     _Pragma("unroll") for (int i = (lo); i < (hi); ++i) {                                                  \
       const bool real_ = GPW * NW == NBLK || wave + i * NW < NBLK;                                         \
-      const uint32_t o_ = i < GW ? dW0 + i * stepW : real_ ? dX0 + (i - GW) * stepX : dXl;                 \
-      const bool ok_ = (k0) + (real_ ? kcol : kcoll) < ke;                                                 \
       const int blk_ = real_ ? wave + i * NW : NBLK - 1;                                                   \
+      uint8_t* const dst_ = smem + (buf) * STAGE + blk_ * 1024;                                            \
       if (i < GW) {                                                                                        \
-        const uint32_t op_ = dWp0 + i * (NW / 2 * 2048) + (uint32_t)((k0) >> 6) * nbw * 2048u;             \
-        const bool okw_ = ok_ && (!wpk || n0 + blk_ * 8 < N);                                               \
-        dma16_nt(rsW, smem + (buf) * STAGE + blk_ * 1024, okw_ ? (wpk ? op_ : o_ + kof_) : kOOB);          \
+        uint32_t o_ = PK ? dWp0 : dW0 + i * stepW;                                                         \
+        if (PK && n0 + BN > N && n0 + blk_ * 8 >= N) o_ = kOOB;                                            \
+        if (part_ && k0_ + kcol >= ke) o_ = kOOB;                                                          \
+        dma16s_nt(rW_, dst_, o_, PK ? skp_ + (uint32_t)(i * (NW / 2 * 2048)) : sk_);                        \
+      } else {                                                                                             \
+        uint32_t o_ = real_ ? dX0 + (i - GW) * stepX : dXl;                                                \
+        if (part_ && k0_ + (real_ ? kcol : kcoll) >= ke) o_ = kOOB;                                        \
+        dma16s(rX_, dst_, o_, sk_);                                                                        \
       }                                                                                                    \
-      else dma16(rsX, smem + (buf) * STAGE + blk_ * 1024, ok_ ? o_ + kof_ : kOOB);                         \
     }                                                                                                      \
   } while (0)
     // Fragment reads. The stationary operand is held for a whole k32 step (both steps' fragments in registers);
@@ -352,9 +364,15 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
 
 template <int FN, int FM, int WN, int WM>
 __global__ void __launch_bounds__(64 * WN * WM) gemm_sk_kernel(const GemmParams p, const int epi) {
-  if (epi == EPI_SILU) sk_body<FN, FM, WN, WM, EPI_SILU>(p);
-  else if (epi == EPI_RESID) sk_body<FN, FM, WN, WM, EPI_RESID>(p);
-  else sk_body<FN, FM, WN, WM, EPI_BF16>(p);  // the host routes EPI_F32 (split-K planes) to other families
+  if (p.wpk) {  // W in the packed layout
+    if (epi == EPI_SILU) sk_body<FN, FM, WN, WM, EPI_SILU, true>(p);
+    else if (epi == EPI_RESID) sk_body<FN, FM, WN, WM, EPI_RESID, true>(p);
+    else sk_body<FN, FM, WN, WM, EPI_BF16, true>(p);  // the host routes EPI_F32 (split-K planes) to other families
+  } else {
+    if (epi == EPI_SILU) sk_body<FN, FM, WN, WM, EPI_SILU, false>(p);
+    else if (epi == EPI_RESID) sk_body<FN, FM, WN, WM, EPI_RESID, false>(p);
+    else sk_body<FN, FM, WN, WM, EPI_BF16, false>(p);
+  }
 }
 
 // Second pass of a stream-K plan: a tile that was split sums its pieces in K order, ((p0 + p1) + p2) + ..., and
