@@ -37,7 +37,7 @@ struct KxShape {
   static constexpr int BN = 16 * FW, BM = 16 * (4 * FX + XE);
   static constexpr int RB = 128, WD = 3;                          // W ring depth (stages of 64 k)
   static constexpr int LDS = (WD * BN + 2 * BM) * RB;             // W ring + x double buffer
-  static constexpr int NW = 8, NBLK = (BN + BM) / 8, GPW = (NBLK + NW - 1) / NW;
+  static constexpr int NW = 8;
   static constexpr int EW = XE == 0 ? 0 : XE == 1 ? (FW + 3) / 4 : (FW + 1) / 2;  // extra W fragments per group
   static constexpr int NX = FX + (XE > 0 ? 1 : 0);                                  // x fragments per wave
   static constexpr int NACC = FW * FX + EW;                                         // accumulators per wave
@@ -154,7 +154,13 @@ __device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&a
 template <int FW, int FX, int XE, int EPI, bool REV, bool PK>
 __device__ __forceinline__ void kx_body(const GemmParams& p) {
   using S = KxShape<FW, FX, XE>;
-  constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW, GPW = S::GPW;
+  constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW;
+  // DMA waves: the waves that issue the operand DMAs. With DWV = 4 only the second wave of each SIMD (h = 1)
+  // issues them, so a wave stalled at a full texture-unit queue leaves its SIMD partner free to keep the MFMA pipe
+  // busy (measured 3-5% faster on the 144 x 64, 144 x 128 and 128 x 288 tiles); the 144 x 288 tile keeps DMAs on
+  // all 8 waves, because 14 slots per DMA wave make it spill (139 us instead of 119 us at gate-up M = 288).
+  constexpr int DWV = (FW == 9 && FX == 4 && XE == 2) ? 8 : 4;
+  constexpr int GPW = ((BN + BM) / 8 + DWV - 1) / DWV;
   constexpr int EW = S::EW, NX = S::NX, NACC = S::NACC, HF = S::HF;
   constexpr int BK = 64;
 
@@ -216,17 +222,19 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   uint8_t* const wring = smem;
   uint8_t* const xring = smem + S::WD * WST;
   constexpr int XB = BM / 8, WB = BN / 8, NB = XB + WB;
-  // Batch slot i (i < GPW) of a wave fetches block c = wave + 8 i of a stage: x block c if c < XB, else W block
-  // c - XB; waves past the end repeat the last block (same bytes to the same place), so every wave issues GPW DMAs
-  // per batch. Only the stage changes from batch to batch: each slot's lane offset at stage 0 is computed once
+  // Batch slot i (i < GPW) of DMA wave dw fetches block c = dw + DWV i of a stage: x block c if c < XB, else W block
+  // c - XB; waves past the end repeat the last block (same bytes to the same place), so every DMA wave issues GPW
+  // DMAs per batch. Only the stage changes from batch to batch: each slot's lane offset at stage 0 is computed once
   // (a VGPR per slot), and the stage's byte offset is a wave-uniform SGPR passed as the DMA's soffset. A stage past
   // the end reads through an empty descriptor (zeros). Slots whose kind (x or W) is the same for every wave are
   // told apart at compile time; at most one slot is x for some waves and W for others.
   uint32_t voff[GPW], lblk[GPW];
   bool isw_[GPW];
+  const bool dmaw = wave >= NW - DWV;
+  const int dw = dmaw ? wave - (NW - DWV) : 0;
 #pragma unroll
   for (int i = 0; i < GPW; ++i) {
-    const int c = min(wave + i * NW, NB - 1);  // wave-uniform
+    const int c = min(dw + i * DWV, NB - 1);  // wave-uniform
     const bool isw = c >= XB;
     const int blk = isw ? c - XB : c, par = blk & 1;
     const int kc = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;  // the chunk's 16-byte swizzle
@@ -258,6 +266,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   }
   // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
   auto dma = [&](int st, int lo, int hi) {
+    if (!dmaw) return;
     const bool ok = st < nk;
     const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in voff
     const uint32_t sw = PK ? (uint32_t)(((kb >> 6) + st) * nbw * 2048) : sx;
@@ -265,7 +274,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
     uint8_t* const xd = xring + (st & 1) * XST;
     uint8_t* const wd = wring + (st % S::WD) * WST;
     auto issue = [&](int i, uint32_t vo) {
-      const bool allx = NW * i + NW - 1 < XB, allw = NW * i >= XB;  // compile-time after unrolling
+      const bool allx = DWV * i + DWV - 1 < XB, allw = DWV * i >= XB;  // compile-time after unrolling
       if (allx || (!allw && !isw_[i])) dma16s(rX, xd + lblk[i], vo, sx);
       else dma16s_nt(rW, wd + lblk[i], vo, sw);
     };
@@ -305,7 +314,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   if (nk > 0) {
     dma(0, 0, GPW);
     dma(1, 0, GPW);
-    wait_vmcnt<GPW>();  // stage 0 has landed
+    if (dmaw) wait_vmcnt<GPW>();  // stage 0 has landed
     kx_barrier();
 #pragma unroll
     for (int i = 0; i < NX; ++i) xc[i] = OJX_KX_RD(xring, xoff[i]);
@@ -329,7 +338,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
     bf16x8 xn[NX], wn[PD];
     const bool more = t + 1 < nk;
     if (more) {
-      wait_vmcnt<GPW>();  // stage t+1 has landed (only the batch of stage t+2 may be outstanding)
+      if (dmaw) wait_vmcnt<GPW>();  // stage t+1 has landed (only the batch of stage t+2 may be outstanding)
       kx_barrier();       // every wave's has, and every wave's W reads of stage t are done
       const uint8_t* nw = wring + ((t + 1) % S::WD) * WST;
       const uint8_t* nx = xring + ((t + 1) & 1) * XST;
