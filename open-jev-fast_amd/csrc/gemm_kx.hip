@@ -155,11 +155,10 @@ template <int FW, int FX, int XE, int EPI, bool REV, bool PK>
 __device__ __forceinline__ void kx_body(const GemmParams& p) {
   using S = KxShape<FW, FX, XE>;
   constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW;
-  // DMA waves: the waves that issue the operand DMAs. With DWV = 4 only the second wave of each SIMD (h = 1)
-  // issues them, so a wave stalled at a full texture-unit queue leaves its SIMD partner free to keep the MFMA pipe
-  // busy (measured 3-5% faster on the 144 x 64, 144 x 128 and 128 x 288 tiles); the 144 x 288 tile keeps DMAs on
-  // all 8 waves, because 14 slots per DMA wave make it spill (139 us instead of 119 us at gate-up M = 288).
-  constexpr int DWV = (FW == 9 && FX == 4 && XE == 2) ? 8 : 4;
+  // DMA waves: the waves that issue the operand DMAs. Only the second wave of each SIMD (h = 1) issues them, so a
+  // wave stalled at a full texture-unit queue leaves its SIMD partner free to keep the MFMA pipe busy (measured
+  // 3-6% faster than DMAs from all 8 waves on the 144 x 64, 144 x 128 and 128 x 288 tiles).
+  constexpr int DWV = 4;
   constexpr int GPW = ((BN + BM) / 8 + DWV - 1) / DWV;
   constexpr int EW = S::EW, NX = S::NX, NACC = S::NACC, HF = S::HF;
   constexpr int BK = 64;
@@ -223,72 +222,57 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   uint8_t* const xring = smem + S::WD * WST;
   constexpr int XB = BM / 8, WB = BN / 8, NB = XB + WB;
   // Batch slot i (i < GPW) of DMA wave dw fetches block c = dw + DWV i of a stage: x block c if c < XB, else W block
-  // c - XB; waves past the end repeat the last block (same bytes to the same place), so every DMA wave issues GPW
-  // DMAs per batch. Only the stage changes from batch to batch: each slot's lane offset at stage 0 is computed once
-  // (a VGPR per slot), and the stage's byte offset is a wave-uniform SGPR passed as the DMA's soffset. A stage past
-  // the end reads through an empty descriptor (zeros). Slots whose kind (x or W) is the same for every wave are
+  // c - XB; past the last block a wave repeats that block (same bytes to the same place), so every DMA wave issues
+  // GPW DMAs per batch. Only the stage changes from batch to batch: the stage's byte offset is a wave-uniform SGPR
+  // passed as the DMA's soffset, and a stage past the end reads through an empty descriptor (zeros). All blocks of
+  // a wave have the parity of dw (DWV and XB are even), hence the same 16-byte chunk swizzle, so a slot's lane
+  // offset is linear in i: one VGPR for x (vx0), one for W (vwr, at the first slot that is W for every wave), a
+  // scalar step each, and one VGPR for the repeated last block. Slots whose kind is the same for every wave are
   // told apart at compile time; at most one slot is x for some waves and W for others.
-  uint32_t voff[GPW], lblk[GPW];
-  bool isw_[GPW];
   const bool dmaw = wave >= NW - DWV;
   const int dw = dmaw ? wave - (NW - DWV) : 0;
-#pragma unroll
-  for (int i = 0; i < GPW; ++i) {
-    const int c = min(dw + i * DWV, NB - 1);  // wave-uniform
-    const bool isw = c >= XB;
-    const int blk = isw ? c - XB : c, par = blk & 1;
-    const int kc = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;  // the chunk's 16-byte swizzle
-    uint32_t o;
-    if (isw) {
-      if constexpr (PK) {  // stage 0, row block (n0 + 8 blk) / 16, rows (8 blk) % 16 .. +7: 1 KiB contiguous
-        const int row = ((n0 >> 4) + (blk >> 1)) * 16 + (blk & 1) * 8 + (lane >> 3);
-        o = n0 + blk * 8 < p.N ? (uint32_t)((row * 64 + kc) * 2) : kOOB;
-      }
-      else
-        o = (uint32_t)(((int64_t)(blk * 8 + (lane >> 3)) * p.ldw + kb + kc) * 2);
-    } else {
-      o = (uint32_t)(((int64_t)(blk * 8 + (lane >> 3)) * p.ldx + kb + kc) * 2);
-    }
-    voff[i] = o;
-    lblk[i] = (uint32_t)(blk * 1024);
-    isw_[i] = isw;
-  }
+  const int lrow = lane >> 3;
+  auto swz = [&](int par) { return ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8; };  // k of the lane's chunk
+  const int kc = swz(dw & 1), kcl = swz((WB - 1) & 1);
+  auto wlane = [&](int blk, int k) -> uint32_t {  // lane offset of W block blk at stage 0 (chunk k)
+    if constexpr (PK) return (uint32_t)(((((n0 >> 4) + (blk >> 1)) * 16 + (blk & 1) * 8 + lrow) * 64 + k) * 2);
+    else return (uint32_t)(((int64_t)(blk * 8 + lrow) * p.ldw + kb + k) * 2);
+  };
+  constexpr int IW = (XB + DWV - 1) / DWV;  // first slot that is W for every wave
+  const uint32_t vx0 = (uint32_t)(((int64_t)(dw * 8 + lrow) * p.ldx + kb + kc) * 2);
+  const uint32_t vwr = wlane(dw + DWV * IW - XB, kc), vlast = wlane(WB - 1, kcl);
+  const uint32_t sxs = (uint32_t)(DWV * 8 * p.ldx * 2);
+  const uint32_t sws = PK ? (uint32_t)(DWV * 1024) : (uint32_t)(DWV * 8 * p.ldw * 2);
   const __amdgpu_buffer_rsrc_t rsNone = make_rsrc(p.W, 0);
-  // A split whose K range is not a multiple of 64 ends in a partial stage, where lanes past ke read zeros: bit i of
-  // tmask says whether this lane's slot i is inside the range at that stage (computed once, outside the loop).
-  const bool ragged = ((ke - kb) & (BK - 1)) != 0;
-  uint32_t tmask = 0;
-#pragma unroll
-  for (int i = 0; i < GPW; ++i) {
-    const int par = (int)(lblk[i] >> 10) & 1;
-    const int kc = ((lane & 7) ^ ((par << 2) | (lane >> 4))) * 8;
-    tmask |= (kb + (nk - 1) * BK + kc < ke ? 1u : 0u) << i;
-  }
+  const bool ragged = ((ke - kb) & (BK - 1)) != 0;  // the last stage is partial: lanes past ke read zeros
+  const bool wedge = PK && n0 + BN > p.N;            // packed: some W blocks of this tile are past N
   // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
   auto dma = [&](int st, int lo, int hi) {
     if (!dmaw) return;
     const bool ok = st < nk;
-    const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in voff
+    const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in the lane offsets
     const uint32_t sw = PK ? (uint32_t)(((kb >> 6) + st) * nbw * 2048) : sx;
     const __amdgpu_buffer_rsrc_t rX = ok ? rsX : rsNone, rW = ok ? rsW : rsNone;
     uint8_t* const xd = xring + (st & 1) * XST;
     uint8_t* const wd = wring + (st % S::WD) * WST;
-    auto issue = [&](int i, uint32_t vo) {
+    const bool tail = ragged && st == nk - 1;  // rare
+#pragma unroll
+    for (int i = 0; i < GPW; ++i) {
+      if (i < lo || i >= hi) continue;
       const bool allx = DWV * i + DWV - 1 < XB, allw = DWV * i >= XB;  // compile-time after unrolling
-      if (allx || (!allw && !isw_[i])) dma16s(rX, xd + lblk[i], vo, sx);
-      else dma16s_nt(rW, wd + lblk[i], vo, sw);
-    };
-    if (ragged && st == nk - 1) {  // rare
-#pragma unroll
-      for (int i = 0; i < GPW; ++i) {
-        if (i < lo || i >= hi) continue;
-        issue(i, (tmask >> i) & 1u ? voff[i] : kOOB);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < GPW; ++i) {
-        if (i < lo || i >= hi) continue;
-        issue(i, voff[i]);
+      const bool mayend = DWV * i + DWV > NB;                          // compile-time: slot may run past NB
+      const int c = dw + DWV * i;                                      // wave-uniform
+      if (allx || (!allw && c < XB)) {
+        uint32_t o = vx0 + (uint32_t)i * sxs;
+        if (tail && kb + st * BK + kc >= ke) o = kOOB;
+        dma16s(rX, xd + c * 1024, o, sx);
+      } else {
+        const bool last = mayend && c >= NB;
+        const int blk = last ? WB - 1 : c - XB;
+        uint32_t o = last ? vlast : vwr + (uint32_t)(i - IW) * sws;
+        if (wedge && n0 + blk * 8 >= p.N) o = kOOB;
+        if (tail && kb + st * BK + (last ? kcl : kc) >= ke) o = kOOB;
+        dma16s_nt(rW, wd + blk * 1024, o, sw);
       }
     }
   };
