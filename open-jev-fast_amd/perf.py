@@ -7,6 +7,8 @@ Algorithmic work per call (fp32 partials and workspace are not counted):
             residual  2 (M K + N K) + 2 M N (residual read) + 2 M N (h write) [+ 2 M N if hn is written]
 Roofline time t = max(bytes / HBM peak, flops / MFMA peak); fraction = t / measured.
 """
+import time
+
 import torch
 
 HBM_PEAK = 8.0e12         # B/s, MI355X HBM3E
@@ -48,10 +50,12 @@ def roofline(M, N, K, kind, seconds, hn=True):
     }
 
 
-def gpu_time(fns, iters=20, reps=5, warmup=2, graph=True):
+def gpu_time(fns, iters=20, reps=5, warmup=2, graph=True, settle=0.2):
     """Average seconds per call of fns[i % len(fns)] (fns rotate over weight copies so each call streams its
     weights from HBM rather than the 256 MB Infinity Cache). Calls are captured in a HIP graph of `iters` calls
-    (as bench/lt_search.py:14-27 does) and timed over `reps` replays with events on the current stream."""
+    (as bench/lt_search.py:14-27 does) and timed over `reps` replays with events on the current stream, after
+    `settle` seconds of untimed replays (a GPU that was idle runs its first replays at lower clocks: measured
+    up to 8% slower on the gate-up at M = 288)."""
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(s):
@@ -71,6 +75,10 @@ def gpu_time(fns, iters=20, reps=5, warmup=2, graph=True):
         def run():
             for i in range(iters):
                 fns[i % len(fns)]()
+    t_end = time.perf_counter() + settle
+    while time.perf_counter() < t_end:
+        run()
+        torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     a.record()
     for _ in range(reps):

@@ -85,7 +85,7 @@ def main():
             def timed(key):
                 try:
                     cc = _lib.cfg(*key)
-                    t = perf.gpu_time([call(w, cc) for w in ws], iters=args.iters, reps=args.reps)
+                    t = perf.gpu_time([call(w, cc) for w in ws], iters=args.iters, reps=args.reps, settle=0.05)
                 except RuntimeError as e:
                     print(json.dumps({"shape": name, "M": M, "cfg": key, "error": str(e)}), flush=True)
                     return
