@@ -119,6 +119,39 @@ def test_argument_validation_without_gpu(pkg):
     assert L.ojx_head_scores(p, 4, 64, p, 0, p, None, p, None) == 0
 
 
+def test_prep_argument_validation_without_gpu(pkg):
+    """The prep entry points reject what their kernels do not handle before any HIP call (head dims, rotary dims,
+    head-count ratios, sizes, alignment); empty inputs are no-ops."""
+    L = pkg._lib.lib()
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    mis = ctypes.c_void_p(p.value + 2)
+    f = ctypes.cast(p, ctypes.POINTER(ctypes.c_float))
+    fa = lambda N, HQ, HKV, D, RD, proj=p: L.ojx_fullattn_prep(proj, N, HQ, HKV, D, RD, 1e-6, f, f, p, p, p, p, p,  # noqa: E731
+                                                                p, None)
+    assert fa(3, 2, 1, 128, 64) == 2 and b"head_dim 256" in L.ojx_last_error()
+    assert fa(3, 2, 1, 256, 48) == 2 and b"rotary" in L.ojx_last_error()   # 48 / 16 = 3, not a power of two
+    assert fa(3, 2, 1, 256, 8) == 2                                          # below 16
+    assert fa(3, 2, 1, 256, 512) == 2                                        # above D
+    assert fa(3, 0, 1, 256, 64) == 2
+    assert fa(3, 2, 1, 256, 64, proj=mis) == 1
+    assert fa(0, 2, 1, 256, 64, proj=None) == 0                              # no tokens: nothing to do
+    q = lambda M, K, RD, w=p: L.ojx_gemm_qkv_fullattn_prep(p, w, 0, f, f, p, p, p, p, p, p, M, K, 2, 1, 256, RD,  # noqa: E731
+                                                           1e-6, None)
+    assert q(4, 256, 32) == 2 and b"RD = 64" in L.ojx_last_error()
+    assert q(4, 260, 64) == 2                                                # K not a multiple of 8
+    assert q(4, 256, 64, w=None) == 1
+    la = lambda N, R, L2, KD, VD, HV, HK, HD, rq, proj=p: L.ojx_linattn_prep(  # noqa: E731
+        proj, p, p, p, N, R, L2, p, p, p, KD, VD, HV, HK, HD, rq, p, p, p, f, p, None)
+    assert la(5, 32, 16, 256, 768, 6, 2, 64, 0) == 2 and b"head_dim 128" in L.ojx_last_error()
+    assert la(5, 32, 16, 384, 768, 6, 2, 128, 0) == 2                       # KD != HK HD
+    assert la(5, 30, 16, 256, 768, 6, 2, 128, 0) == 2                       # R not a multiple of L2
+    assert la(5, 32, 16, 256, 768, 8, 2, 128, 1) == 2 and b"HV / HK = 3" in L.ojx_last_error()
+    assert la(5, 32, 16, 256, 768, 300, 2, 128, 0) == 2                     # HV > 256
+    assert la(5, 32, 16, 256, 768, 6, 2, 128, 0, proj=mis) == 1
+    assert la(5, 0, 16, 256, 768, 6, 2, 128, 0, proj=None) == 0             # no slots: nothing to do
+
+
 def test_python_mirror_errors_without_gpu(pkg):
     import torch
     from importlib import import_module
