@@ -919,6 +919,8 @@ static const TileEntry kTiles[] = {
     OJX_KX(8, 1, 0),                // 87 128 x 64
     OJX_KX(16, 2, 0),               // 88 256 x 128: one 256-dim attention head per tile (prep epilogue)
     OJX_KX(16, 1, 0),               // 89 256 x 64
+    OJX_TILE(32, 16, 128, 2, 1),    // 90 skinny M, 32 W rows: N / 32 workgroups without split-K
+    OJX_TILE(32, 16, 256, 2, 1),    // 91 the same, deeper K stages
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];
