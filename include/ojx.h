@@ -168,7 +168,9 @@ int ojx_gemm_qkv_fullattn_prep(const void* x, const void* w, int32_t w_packed, c
  * q, k bf16 [R, RQ KD] with RQ = HV / HK (3) when rep_qk != 0 else 1, v bf16 [R, VD], g fp32 [R, HV], beta bf16
  * [R, HV]. Depthwise causal conv (4 taps) + SiLU, L2 norm of each q / k head, beta = sigmoid(b),
  * g = -exp(A_log) softplus(a + dt_bias); each packed row computed once and written to every slot holding it; the
- * end-padding slots get zeros. HD = 128, KD = HK HD, R a multiple of L2, HV <= 256; every pointer 16-byte aligned. */
+ * end-padding slots get zeros. HD = 128, KD = HK HD, R a multiple of L2, HV <= 256; every pointer 16-byte aligned.
+ * The index arrays are used as given (as in the reference): rep_ptr non-decreasing with rep_ptr[N + 1] <= R,
+ * rep_pos entries in [0, R), hist entries -1 or in [0, N). */
 int ojx_linattn_prep(const void* proj, const int32_t* hist, const int32_t* rep_ptr, const int32_t* rep_pos,
                      int64_t N, int64_t R, int64_t L2, const void* convw, const void* A_log, const void* dt_bias,
                      int32_t KD, int32_t VD, int32_t HV, int32_t HK, int32_t HD, int32_t rep_qk, void* q, void* k,

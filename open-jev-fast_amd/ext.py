@@ -331,6 +331,14 @@ def _prep_outputs(N, HQ, HKV, D, like):
     return qt, kt, vt, gate
 
 
+def _chk_rope(qw1, kw1, cos, sin, N, D):
+    """The norm weights are [D] and cos / sin [N, RD] (the kernels read N rows of RD and D weights)."""
+    if qw1.numel() != D or kw1.numel() != D:
+        raise RuntimeError(f"qw1 and kw1 must have D={D} elements, got {qw1.numel()} and {kw1.numel()}")
+    if cos.dim() != 2 or tuple(cos.shape) != tuple(sin.shape) or cos.shape[0] != N:
+        raise RuntimeError(f"cos and sin must both be [N={N}, RD], got {tuple(cos.shape)} and {tuple(sin.shape)}")
+
+
 def fullattn_prep2(proj, qw1, kw1, cos, sin, B, T, HQ, HKV, D, eps):
     """The reference extension's fullattn_prep2 (src/kernels.cu:302-360) for B = 1 (the tree forward's call,
     src/fastmodel.py:462): [qt [1, HQ, T, D], kt [1, HKV, T, D], vt [1, HKV, T, D], gate [T, HQ D]]."""
@@ -344,6 +352,7 @@ def fullattn_prep2(proj, qw1, kw1, cos, sin, B, T, HQ, HKV, D, eps):
     N = proj.shape[0]
     if N != T or proj.shape[1] != (2 * HQ + 2 * HKV) * D:
         raise RuntimeError(f"proj {tuple(proj.shape)} does not match T={T}, HQ={HQ}, HKV={HKV}, D={D}")
+    _chk_rope(qw1, kw1, cos, sin, N, D)
     RD = cos.shape[1]
     qt, kt, vt, gate = _prep_outputs(N, HQ, HKV, D, proj)
     check(lib().ojx_fullattn_prep(_ptr(proj), N, HQ, HKV, D, RD, float(eps), _ptr(qw1), _ptr(kw1), _ptr(cos),
@@ -395,6 +404,7 @@ def mm_fullattn_prep(x, w_qkv, qw1, kw1, cos, sin, HQ, HKV, D, eps):
     N, Kw = _pk_shape(w_qkv) if packed else tuple(w_qkv.shape)
     if Kw != K or N != (2 * HQ + 2 * HKV) * D:
         raise RuntimeError(f"w_qkv does not match x {tuple(x.shape)}, HQ={HQ}, HKV={HKV}, D={D}")
+    _chk_rope(qw1, kw1, cos, sin, M, D)
     qt, kt, vt, gate = _prep_outputs(M, HQ, HKV, D, x)
     check(lib().ojx_gemm_qkv_fullattn_prep(_ptr(x), _ptr(w_qkv), int(packed), _ptr(qw1), _ptr(kw1), _ptr(cos),
                                            _ptr(sin), _ptr(qt), _ptr(kt), _ptr(vt), _ptr(gate), M, K, HQ, HKV, D,

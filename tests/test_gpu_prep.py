@@ -78,6 +78,10 @@ def test_fullattn_prep_rejects(ext, dev):
         ext.fullattn_prep2(proj, qw1, kw1, cos, sin, 2, 3, 2, 1, 256, EPS)  # B != 1
     with pytest.raises(RuntimeError):
         ext.fullattn_prep2(proj, qw1, kw1, cos[:, :48].contiguous(), sin[:, :48].contiguous(), 1, 3, 2, 1, 256, EPS)
+    with pytest.raises(RuntimeError, match="cos and sin"):  # fewer cos rows than tokens
+        ext.fullattn_prep2(proj, qw1, kw1, cos[:2].contiguous(), sin[:2].contiguous(), 1, 3, 2, 1, 256, EPS)
+    with pytest.raises(RuntimeError, match="qw1 and kw1"):
+        ext.fullattn_prep2(proj, qw1[:128].contiguous(), kw1, cos, sin, 1, 3, 2, 1, 256, EPS)
     empty = torch.empty(0, proj.shape[1], dtype=proj.dtype, device=dev)
     out = ext.fullattn_prep2(empty, qw1, kw1, cos[:0], sin[:0], 1, 0, 2, 1, 256, EPS)
     assert out[0].shape[2] == 0
