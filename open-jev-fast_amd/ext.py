@@ -86,19 +86,30 @@ def _workspace(M, N, K, kind, cfg, device):
     return buf, buf.numel()
 
 
+def _chk_norm(w1, rowmask, M, H):
+    """RMSNorm operands: w1 fp32 [H]; rowmask (optional) int32 [M]. The kernels read exactly that many."""
+    _chk(w1, "w1", torch.float32)
+    if w1.numel() != H:
+        raise RuntimeError(f"w1 must have H={H} elements, got {w1.numel()}")
+    if rowmask is not None:
+        _chk(rowmask, "rowmask", torch.int32)
+        if rowmask.numel() != M:
+            raise RuntimeError(f"rowmask must have M={M} elements, got {rowmask.numel()}")
+
+
 # ------------------------------------------------------------------------------------------------ epilogues
 def add_rmsnorm(x, delta, w1, rowmask, eps):
     _chk(x, "x", torch.bfloat16)
-    _chk(w1, "w1", torch.float32)
     M, H = x.shape
+    _chk_norm(w1, rowmask, M, H)
     hn = torch.empty_like(x)
     if delta is not None:
         _chk(delta, "delta", torch.bfloat16)
+        if tuple(delta.shape) != (M, H):
+            raise RuntimeError(f"delta {tuple(delta.shape)} must match x {tuple(x.shape)}")
         h = torch.empty_like(x)
     else:
         h = x
-    if rowmask is not None:
-        _chk(rowmask, "rowmask", torch.int32)
     check(lib().ojx_add_rmsnorm(_ptr(x), _ptr(delta), _ptr(w1), _ptr(rowmask), float(eps),
                                 _ptr(h) if delta is not None else None, _ptr(hn), M, H, _stream()))
     return [h, hn]
@@ -107,13 +118,11 @@ def add_rmsnorm(x, delta, w1, rowmask, eps):
 def add_rmsnorm_sk(x, parts, w1, rowmask, eps):
     _chk(x, "x", torch.bfloat16)
     _chk(parts, "parts", torch.float32)
-    _chk(w1, "w1", torch.float32)
     M, H = x.shape
+    _chk_norm(w1, rowmask, M, H)
     S = parts.shape[0]
     if parts.dim() != 3 or parts.shape[1] != M or parts.shape[2] != H:
         raise RuntimeError("parts must be [S, M, H]")
-    if rowmask is not None:
-        _chk(rowmask, "rowmask", torch.int32)
     h, hn = torch.empty_like(x), torch.empty_like(x)
     check(lib().ojx_add_rmsnorm_sk(_ptr(x), _ptr(parts), S, _ptr(w1), _ptr(rowmask), float(eps), _ptr(h), _ptr(hn),
                                    M, H, _stream()))
@@ -211,8 +220,8 @@ def mm_residual_rmsnorm(h, y, w, w1, rowmask, eps, want_hn=True, cfg=None):
     if w.shape[1] != K or tuple(h.shape) != (M, N):
         raise RuntimeError(f"shape mismatch: h {tuple(h.shape)} y {tuple(y.shape)} w {tuple(w.shape)}")
     if want_hn:
-        _chk(w1, "w1", torch.float32)
-    if rowmask is not None:
+        _chk_norm(w1, rowmask, M, N)
+    elif rowmask is not None:
         _chk(rowmask, "rowmask", torch.int32)
     h_new = torch.empty_like(h)
     hn = torch.empty_like(h) if want_hn else None
@@ -310,8 +319,8 @@ def mm_residual_rmsnorm_pk(h, y, wp, w1, rowmask, eps, want_hn=True, cfg=None):
     if y.shape[1] != K or tuple(h.shape) != (M, N):
         raise RuntimeError(f"shape mismatch: h {tuple(h.shape)} y {tuple(y.shape)}, packed weight N={N} K={K}")
     if want_hn:
-        _chk(w1, "w1", torch.float32)
-    if rowmask is not None:
+        _chk_norm(w1, rowmask, M, N)
+    elif rowmask is not None:
         _chk(rowmask, "rowmask", torch.int32)
     h_new = torch.empty_like(h)
     hn = torch.empty_like(h) if want_hn else None
