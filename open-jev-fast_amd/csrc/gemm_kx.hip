@@ -249,6 +249,9 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   // DMAs lo .. hi-1 of the batch that fetches stage st (x into x slot st & 1, W into W slot st % WD)
   auto dma = [&](int st, int lo, int hi) {
     if (!dmaw) return;
+    // the issuing wave goes first while it issues (its SIMD partner's MFMAs wait a few cycles, the DMAs leave
+    // sooner): measured 2-5% faster on the 144 x 128 and 128 x 288 tiles
+    __builtin_amdgcn_s_setprio(2);
     const bool ok = st < nk;
     const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in the lane offsets
     const uint32_t sw = PK ? (uint32_t)(((kb >> 6) + st) * nbw * 2048) : sx;
@@ -275,6 +278,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
         dma16s_nt(rW, wd + blk * 1024, o, sw);
       }
     }
+    __builtin_amdgcn_s_setprio(0);
   };
 
   f32x4 acc[FW][FX], acce[EW > 0 ? EW : 1];
