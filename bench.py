@@ -340,7 +340,8 @@ def main_prep(args, pkg, ext, perf):
         sin = torch.cat([ang.sin(), ang.sin()], 1).bfloat16()
         proj = ext.mm(x, ws[0])
         two = [lambda w=w: ext.fullattn_prep2(ext.mm(x, w), qw1, kw1, cos, sin, 1, M, HQ, HKV, D, 1e-6) for w in ws]
-        fused = [lambda w=w: ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, HQ, HKV, D, 1e-6) for w in ws]
+        fused = [lambda w=w: ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, HQ, HKV, D, 1e-6, fused=True)
+                 for w in ws]
         gemm = [lambda w=w: ext.mm(x, w) for w in ws]
         prep = [lambda: ext.fullattn_prep2(proj, qw1, kw1, cos, sin, 1, M, HQ, HKV, D, 1e-6)]
         t = {k: min(perf.gpu_time(f, iters=10, reps=3), perf.gpu_time(f, iters=10, reps=3))

@@ -399,10 +399,17 @@ def linattn_prep_dedup2(proj, hist, rep_ptr, rep_pos, L2, convw, A_log, dt_bias,
     return [q, k, v, g, beta]
 
 
-def mm_fullattn_prep(x, w_qkv, qw1, kw1, cos, sin, HQ, HKV, D, eps):
-    """_mm(hn, d.w_in) + fullattn_prep2 in one kernel (src/fastmodel.py:412,462): the QKV in-projection with the
-    prep in its epilogue. w_qkv row-major [(2 HQ + 2 HKV) D, K] or packed (pack_weight). Returns the prep's outputs
-    [qt [1, HQ, M, D], kt, vt, gate [M, HQ D]]."""
+def mm_fullattn_prep(x, w_qkv, qw1, kw1, cos, sin, HQ, HKV, D, eps, fused=False):
+    """_mm(hn, d.w_in) + fullattn_prep2 (src/fastmodel.py:412,462): the QKV in-projection and the full-attention
+    prep. w_qkv row-major [(2 HQ + 2 HKV) D, K] or packed (pack_weight). Returns the prep's outputs
+    [qt [1, HQ, M, D], kt, vt, gate [M, HQ D]]. By default the planned GEMM followed by the prep kernel (two
+    launches, the faster route at every measured M); fused=True runs ojx_gemm_qkv_fullattn_prep, the prep in the
+    GEMM's epilogue (one launch, the [M, (2 HQ + 2 HKV) D] projection never stored)."""
+    if not fused:
+        rows = _pk_shape(w_qkv)[0] if w_qkv.dim() == 4 else w_qkv.shape[0]
+        if rows != (2 * HQ + 2 * HKV) * D:
+            raise RuntimeError(f"w_qkv does not match x {tuple(x.shape)}, HQ={HQ}, HKV={HKV}, D={D}")
+        return fullattn_prep2(mm(x, w_qkv), qw1, kw1, cos, sin, 1, x.shape[0], HQ, HKV, D, eps)
     _chk(x, "x", torch.bfloat16)
     for t, nm in ((qw1, "qw1"), (kw1, "kw1")):
         _chk(t, nm, torch.float32)

@@ -99,7 +99,7 @@ def test_gemm_qkv_fullattn_prep(pkg, ext, O, dev, M, HQ, HKV, K, packed):
     xd, wd = x.to(dev), w.to(dev)
     qd, kd, cd, sd = qw1.to(dev), kw1.to(dev), cos.to(dev), sin.to(dev)
     wuse = ext.pack_weight(wd) if packed else wd
-    qt, kt, vt, gate = ext.mm_fullattn_prep(xd, wuse, qd, kd, cd, sd, HQ, HKV, D, EPS)
+    qt, kt, vt, gate = ext.mm_fullattn_prep(xd, wuse, qd, kd, cd, sd, HQ, HKV, D, EPS, fused=True)
     # (b) the unfused chain with the same tile: the projection is identical, the prep's sum order differs
     tile = 89 if M <= 64 else 88
     proj = (ext.mm_pk if packed else ext.mm)(xd, wuse, cfg=(tile, 1))
@@ -108,16 +108,20 @@ def test_gemm_qkv_fullattn_prep(pkg, ext, O, dev, M, HQ, HKV, K, packed):
     assert torch.equal(vt.cpu(), uv.cpu()) and torch.equal(gate.cpu(), ug.cpu())
     _close_bf16(qt[0], uq[0], "fused q vs unfused")
     _close_bf16(kt[0], uk[0], "fused k vs unfused")
+    # the default route (planned GEMM, then the prep kernel) against the same oracle chain below
+    dq, dk, dv, dg = ext.mm_fullattn_prep(xd, wuse, qd, kd, cd, sd, HQ, HKV, D, EPS)
     # (a) the oracle chain on the north star's tolerance
     rq, rk, rv, rg = O.fullattn_prep(O.linear_bf16(x, w), qw1, kw1, cos, sin, HQ, HKV, D, EPS)
-    for got, ref, nm in ((qt[0], rq, "q"), (kt[0], rk, "k"), (vt[0], rv, "v"), (gate, rg, "gate")):
+    for got, ref, nm in ((qt[0], rq, "q"), (kt[0], rk, "k"), (vt[0], rv, "v"), (gate, rg, "gate"),
+                         (dq[0], rq, "q, two launches"), (dk[0], rk, "k, two launches"), (dv[0], rv, "v, two launches"),
+                         (dg, rg, "gate, two launches")):
         _assert_tol(O, got, ref, f"{nm} M={M}")
 
 
 def test_gemm_qkv_fullattn_prep_rejects(ext, dev):
     x, w, qw1, kw1, cos, sin = [t.to(dev) for t in _inputs(4, 2, 1, 256, 32, seed=2, K=256)]
     with pytest.raises(RuntimeError):  # the fused epilogue handles RD = 64 only
-        ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, 2, 1, 256, EPS)
+        ext.mm_fullattn_prep(x, w, qw1, kw1, cos, sin, 2, 1, 256, EPS, fused=True)
     with pytest.raises(RuntimeError):  # weight rows do not match the head counts
         ext.mm_fullattn_prep(x, w[:512].contiguous(), qw1, kw1, cos, sin, 2, 1, 256, EPS)
 
