@@ -74,8 +74,8 @@ def measure_shape(ext, perf, name, M, iters=20, reps=5):
 
 
 def cpu_baseline(M, I, K, budget_s=15.0):
-    """The oracle's CPU path (BASELINE.md plan: torch.matmul on bf16 CPU tensors + the same SiLU.mul epilogue) on
-    a row slice of W_gu sized to about `budget_s` seconds; median of 5 after 2 warm-ups."""
+    """The oracle's CPU path (the reported CPU baseline: torch.matmul on bf16 CPU tensors + the same SiLU.mul
+    epilogue) on a row slice of W_gu sized to about `budget_s` seconds; median of 5 after 2 warm-ups."""
     from oracle import proj_oracle as O
     torch.set_num_threads(os.cpu_count() or 1)
     g = torch.Generator().manual_seed(0)
