@@ -2,7 +2,8 @@
 configuration), row-major and packed weights, against the CPU oracle, through the C-ABI.
 
 Each case draws M in [1, 700], N a multiple of 16 in [16, 3072] (gate-up: 2 I with I a multiple of 8), K a multiple
-of 64 in [64, 2048] from a fixed seed, so the set is the same on every run. Tolerance:
+of 64 in [64, 2048] (and, row-major only, a multiple of 8 in [8, 2400]) from a fixed seed, so the set is the same on
+every run. Tolerance:
 max |out - ref| / max |ref| <= 1e-2 and mean |out - ref| <= 1e-3 * RMS(ref).
 """
 import random
@@ -27,12 +28,19 @@ def _cases(n=48, seed=2026):
     return out
 
 
+def _ragged_cases(n=24, seed=7):
+    """Row-major weights with K only a multiple of 8: the kernels' partial last K stage."""
+    r = random.Random(seed)
+    return [(("plain", "silu", "residual")[i % 3], r.randint(1, 700), 16 * r.randint(1, 192), 8 * r.randint(1, 300),
+             False) for i in range(n)]
+
+
 def _tol(O, out, ref, what):
     ok, a, b = O.tolerance_ok(out.float().cpu(), ref.float().cpu(), **TOL)
     assert ok, f"{what}: max_rel {a:.3e} mean/rms {b:.3e}"
 
 
-@pytest.mark.parametrize("kind,M,N,K,packed", _cases())
+@pytest.mark.parametrize("kind,M,N,K,packed", _cases() + _ragged_cases())
 def test_planned_call_random_shape(ext, O, dev, kind, M, N, K, packed):
     print(f"case {kind} M={M} N={N} K={K} packed={packed}", flush=True)
     x, w = O.seeded_inputs(M, N, K, seed=M * 7 + N + K)
