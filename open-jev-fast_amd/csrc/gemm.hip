@@ -811,9 +811,9 @@ struct TileEntry {
 #define OJX_W32D(FN, FM, WN, WM, DG)                                                                         \
   {{WN * FN * 32, WM * FM * 32, 64, WN, WM, 64 * WN * WM, 2 * (WM * FM * 32) * 128, 4},                      \
    gemm_w32d_kernel<FN, FM, WN, WM, DG>}
-// Persistent stream-K tiles: BN = WN*FN*16 W rows, BM = WM*FM*16 x rows, 64-k stages, two LDS buffers
+// Persistent stream-K tiles: BN = WN*FN*16 W rows, BM = WM*FM*16 x rows, 64-k stages, two or three LDS buffers
 #define OJX_SK(FN, FM, WN, WM)                                                                               \
-  {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, 2 * (WN * FN * 16 + WM * FM * 16) * 128, 5},    \
+  {{WN * FN * 16, WM * FM * 16, 64, WN, WM, 64 * WN * WM, sk_lds(WN * FN * 16, WM * FM * 16), 5},          \
    gemm_sk_kernel<FN, FM, WN, WM>, gemm_sk_fixup_kernel<FN, FM, WN, WM>,                                   \
    gemm_sk_fixup_rmsnorm_kernel<FN, FM, WN, WM>}
 // K-interleaved pair tiles: BN = 16 FW W rows, BM = 16 (4 FX + XE) x rows, 8 waves, 64-k stages, two LDS buffers

@@ -168,6 +168,9 @@ __global__ void gemm_sk_fixup_kernel(const GemmParams p, const int epi);
 template <int FN, int FM, int WN, int WM>
 __global__ void gemm_sk_fixup_rmsnorm_kernel(const GemmParams p, const float* w1, const int32_t* rowmask, float eps,
                                              uint16_t* hn_out);
+// Its dynamic LDS: 3 stage buffers of (BN + BM) rows x 128 B where they fit in 160 KiB, else 2.
+constexpr int sk_nbuf(int BN, int BM) { return 3 * (BN + BM) * 128 <= 160 * 1024 ? 3 : 2; }
+constexpr int sk_lds(int BN, int BM) { return sk_nbuf(BN, BM) * (BN + BM) * 128; }
 // K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
 template <int FW, int FX, int XE>
 __global__ void gemm_kx_kernel(const GemmParams p, const int epi);
