@@ -12,7 +12,8 @@
 //   * Both operand tiles go global -> LDS by DMA (buffer_load ... lds, 16 B per lane, one 8-row x 128 B block per
 //     wave instruction) in stages of 64 k, three LDS buffers where they fit (stages t+1 and t+2 in flight while
 //     stage t is multiplied, so a wave's DMA queue does not drain at each stage's barrier: 3-20% faster on the
-//     256 x 96, 256 x 128 and 128 x 288 tiles), else two; no registers are spent on staging. LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row / 2) mod
+//     256 x 96, 256 x 128 and 128 x 288 tiles), else two (256 x 192: a ring of three W stages beside two x stages,
+//     W a stage further ahead, 3-6% faster); no registers are spent on staging. LDS rows are 128 B with the 16-byte chunks XOR-swizzled by (row / 2) mod
 //     8, so the 16 rows that one ds_read_b128 touches land on 16 distinct bank groups. (Stages of 32 k with four
 //     buffers were measured slower: twice the barriers, and no gain from the deeper DMA queue.) Half of a stage's
 //     DMA instructions go out after the barrier that frees their buffer, the rest one per MFMA group of the next
@@ -83,7 +84,12 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
   // LDS stage buffers: 3 where they fit, so that the DMAs run two stages ahead and a wave's queue never drains at
   // the end of a stage; else 2 (one stage ahead)
   constexpr int NBUF = sk_nbuf(BN, BM);
-  static_assert(NBUF * STAGE == sk_lds(BN, BM), "LDS layout");
+  // ASYM (two stage buffers only): W in a ring of 3 stages and x in a ring of 2; a DMA batch carries x of its stage
+  // and W of the next one, x first, so that W runs a stage further ahead and the wait for a stage leaves the next
+  // stage's W in flight
+  constexpr bool ASYM = sk_asym(BN, BM);
+  constexpr int WST = BN * RB, XST = BM * RB;
+  static_assert(sk_lds(BN, BM) == (ASYM ? 3 * WST + 2 * XST : NBUF * STAGE), "LDS layout");
   constexpr int NBLK = ROWS / 8;                // 8-row blocks per stage: one DMA instruction each
   constexpr int GPW = (NBLK + NW - 1) / NW;     // DMA instructions per wave and stage
   constexpr int GW = BN / 8 / NW;               // of which W blocks
@@ -125,7 +131,17 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
   // fragment reads: row r0 + lr (r0 a multiple of 16), logical chunk 4 s + lg of k32 step s
   const uint32_t ro0 = (uint32_t)(lr * RB + ((lg ^ (lr >> 1)) * 16));
   const uint32_t ro1 = (uint32_t)(lr * RB + (((4 + lg) ^ (lr >> 1)) * 16));
-  const uint32_t wbase = (uint32_t)(wn * FN * 16 * RB), xbase = (uint32_t)((BN + wm * FM * 16) * RB);
+  const uint32_t wbase = (uint32_t)(wn * FN * 16 * RB), xbase = (uint32_t)(wm * FM * 16 * RB);
+  // W and x of stage s in LDS (two or three stage buffers of W rows then x rows; ASYM: a W ring of 3, then an x
+  // ring of 2)
+  auto wptr = [&](int s) -> uint8_t* {
+    if constexpr (ASYM) return smem + ((s + 3) % 3) * WST;  // s >= -1
+    else return smem + (NBUF == 3 ? s % 3 : s & 1) * STAGE;
+  };
+  auto xptr = [&](int s) -> uint8_t* {
+    if constexpr (ASYM) return smem + 3 * WST + (s & 1) * XST;
+    else return smem + (NBUF == 3 ? s % 3 : s & 1) * STAGE + WST;
+  };
 
   // stream-K range of this workgroup
   const int64_t T = (int64_t)(tiles - dp) * ipt;
@@ -178,29 +194,36 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     // wave-uniform and goes in the DMA's soffset; only the row-major block offset costs a vector add. A stage past
     // the segment reads zeros through an empty descriptor, W blocks past N (packed) likewise; only a partial last
     // stage (a K range that is not a multiple of 64) needs per-lane checks, on a separate path.
-#define OJX_SK_DMA(buf, k0, lo, hi)                                                                        \
+#define OJX_SK_DMA(s, lo, hi) OJX_SK_DMAW(s, lo, hi, false)
+  // issue position j -> slot i: W slots (i < GW) first, or with ASYM the x slots first
+#define OJX_SK_SLOT(j) (ASYM ? ((j) < GPW - GW ? GW + (j) : (j) - (GPW - GW)) : (j))
+  // batch s: x of stage s and W of stage s (ASYM: s + 1); wonly: the W slots only
+#define OJX_SK_DMAW(s, lo, hi, wonly)                                                                      \
   do {                                                                                                     \
-    const int k0_ = (k0);                                                                                  \
-    const bool live_ = k0_ < ke;                                                                           \
-    const bool part_ = live_ && k0_ + BK > ke;                                                             \
-    const uint32_t sk_ = (uint32_t)k0_ * 2u;                                                               \
-    const uint32_t skp_ = (uint32_t)(k0_ >> 6) * (uint32_t)nbw * 2048u;                                    \
-    const __amdgpu_buffer_rsrc_t rX_ = live_ ? rsX : rsNone, rW_ = live_ ? rsW : rsNone;                   \
+    const int sx_ = (s), sw_ = ASYM ? sx_ + 1 : sx_;                                                       \
+    const int kx_ = kb + sx_ * BK, kw_ = kb + sw_ * BK;                                                    \
+    const bool livex_ = kx_ < ke, livew_ = kw_ < ke;                                                       \
+    const bool partx_ = livex_ && kx_ + BK > ke, partw_ = livew_ && kw_ + BK > ke;                         \
+    const uint32_t skx_ = (uint32_t)kx_ * 2u, skw_ = (uint32_t)kw_ * 2u;                                   \
+    const uint32_t skp_ = (uint32_t)(kw_ >> 6) * (uint32_t)nbw * 2048u;                                    \
+    const __amdgpu_buffer_rsrc_t rX_ = livex_ ? rsX : rsNone, rW_ = livew_ ? rsW : rsNone;                 \
+    uint8_t* const wd_ = wptr(sw_);                                                                        \
+    uint8_t* const xd_ = xptr(sx_) - BN * RB;  /* x block gi >= BN / 8 at xd_ + gi KiB */                   \
     /* keep the per-block offsets as one multiply-add each instead of GPW registers held across the loop */ \
     asm volatile("" : "+s"(stepW), "+s"(stepX));                                                           \
-    _Pragma("unroll") for (int i = (lo); i < (hi); ++i) {                                                  \
+    _Pragma("unroll") for (int j = (lo); j < (hi); ++j) {                                                  \
+      const int i = OJX_SK_SLOT(j);                                                                        \
       const bool real_ = GPW * NW == NBLK || wave + i * NW < NBLK;                                         \
       const int blk_ = real_ ? wave + i * NW : NBLK - 1;                                                   \
-      uint8_t* const dst_ = smem + (buf) * STAGE + blk_ * 1024;                                            \
       if (i < GW) {                                                                                        \
         uint32_t o_ = PK ? dWp0 : dW0 + i * stepW;                                                         \
         if (PK && n0 + BN > N && n0 + blk_ * 8 >= N) o_ = kOOB;                                            \
-        if (part_ && k0_ + kcol >= ke) o_ = kOOB;                                                          \
-        dma16s_nt(rW_, dst_, o_, PK ? skp_ + (uint32_t)(i * (NW / 2 * 2048)) : sk_);                        \
-      } else {                                                                                             \
+        if (partw_ && kw_ + kcol >= ke) o_ = kOOB;                                                         \
+        dma16s_nt(rW_, wd_ + blk_ * 1024, o_, PK ? skp_ + (uint32_t)(i * (NW / 2 * 2048)) : skw_);          \
+      } else if (!(wonly)) {                                                                               \
         uint32_t o_ = real_ ? dX0 + (i - GW) * stepX : dXl;                                                \
-        if (part_ && k0_ + (real_ ? kcol : kcoll) >= ke) o_ = kOOB;                                        \
-        dma16s(rX_, dst_, o_, sk_);                                                                        \
+        if (partx_ && kx_ + (real_ ? kcol : kcoll) >= ke) o_ = kOOB;                                       \
+        dma16s(rX_, xd_ + blk_ * 1024, o_, skx_);                                                          \
       }                                                                                                    \
     }                                                                                                      \
   } while (0)
@@ -212,8 +235,9 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     constexpr bool XST = FM < FN;
     constexpr int NS = XST ? FM : FN, NR = XST ? FN : FM;
 #define OJX_SK_FRAG(sb, base, st, f) (*reinterpret_cast<const bf16x8*>((sb) + (base) + ((st) ? ro1 : ro0) + (f) * 16 * RB))
-#define OJX_SK_S(sb, st, q) OJX_SK_FRAG(sb, XST ? xbase : wbase, st, q)
-#define OJX_SK_R(sb, g) OJX_SK_FRAG(sb, XST ? wbase : xbase, (g) / NR, (g) % NR)
+  // fragments of stage s: the stationary operand's (S) and the streaming operand's (R)
+#define OJX_SK_S(s, st, q) OJX_SK_FRAG(XST ? xptr(s) : wptr(s), XST ? xbase : wbase, st, q)
+#define OJX_SK_R(s, g) OJX_SK_FRAG(XST ? wptr(s) : xptr(s), XST ? wbase : xbase, (g) / NR, (g) % NR)
 #define OJX_SK_MFMA(q, r, sv, rv)                                                                          \
   do {                                                                                                     \
     if constexpr (XST) acc[r][q] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(rv, sv, acc[r][q], 0, 0, 0);    \
@@ -239,28 +263,31 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
     constexpr int H0 = NA <= 0 ? GPW : (GPW - NA > (GPW + 1) / 2 ? GPW - NA : (GPW + 1) / 2);
     constexpr int DPG = H0 < GPW ? 1 : 0;          // DMAs per group
     constexpr int NDG = GPW - H0;                  // groups that carry one
-    auto bidx = [](int t) { return NBUF == 3 ? t % 3 : t & 1; };
-    OJX_SK_DMA(0, kb, 0, GPW);
-    if constexpr (NBUF == 3) {
-      OJX_SK_DMA(1, kb + BK, 0, GPW);
-      OJX_SK_DMA(2, kb + 2 * BK, 0, H0);  // the rest of stage 2 in stage 0's groups (zeros past ke)
-      wait_vmcnt<GPW + H0>();             // stage 0 has landed; stages 1 and 2 may be in flight
+    if constexpr (ASYM) {
+      OJX_SK_DMAW(-1, 0, GPW, true);  // W of stage 0
+      OJX_SK_DMA(0, 0, GPW);          // x of stage 0, then W of stage 1
+      OJX_SK_DMA(1, 0, H0);           // the rest of batch 1 in stage 0's groups (zeros past ke)
+      wait_vmcnt<GW + H0>();          // W and x of stage 0 have landed
+    } else if constexpr (NBUF == 3) {
+      OJX_SK_DMA(0, 0, GPW);
+      OJX_SK_DMA(1, 0, GPW);
+      OJX_SK_DMA(2, 0, H0);           // the rest of stage 2 in stage 0's groups (zeros past ke)
+      wait_vmcnt<GPW + H0>();         // stage 0 has landed; stages 1 and 2 may be in flight
     } else {
-      OJX_SK_DMA(1, kb + BK, 0, H0);  // the rest of stage 1 in stage 0's groups (zeros past ke)
+      OJX_SK_DMA(0, 0, GPW);
+      OJX_SK_DMA(1, 0, H0);           // the rest of stage 1 in stage 0's groups (zeros past ke)
       wait_vmcnt<H0>();               // stage 0 has landed; stage 1 may be in flight
     }
     dma_barrier();
     bf16x8 s0c[NS], rn[PD];
 #pragma unroll
-    for (int q = 0; q < NS; ++q) s0c[q] = OJX_SK_S(smem, 0, q);
+    for (int q = 0; q < NS; ++q) s0c[q] = OJX_SK_S(0, 0, q);
 #pragma unroll
-    for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(smem, d);
+    for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(0, d);
     for (int t = 0; t < nk; ++t) {
-      const uint8_t* sb = smem + bidx(t) * STAGE;
-      // the stage whose DMAs this stage's groups carry (t+1, or t+2 with three buffers), into a buffer not read in
-      // this stage; past the segment's last stage the DMAs read zeros into an unused buffer
-      const int kn = kb + (t + NBUF - 1) * BK;
-      const int bn = bidx(t + NBUF - 1);
+      // the batch this stage's groups carry (t+1, or t+2 with three buffers), into buffers not read in this
+      // stage; past the segment's last stage the DMAs read zeros into unused buffers
+      const int ta = t + NBUF - 1;
       bf16x8 s1c[NS], rr[XR];
 #pragma unroll
       for (int d = 0; d < PD; ++d) rr[d] = rn[d];
@@ -268,25 +295,25 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
       for (int g = 0; g < NMG; ++g) {
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq)
-          if ((qq * NR) / NS == g) s1c[qq] = OJX_SK_S(sb, 1, qq);
-        rr[(g + PD) % XR] = OJX_SK_R(sb, g + PD);
+          if ((qq * NR) / NS == g) s1c[qq] = OJX_SK_S(t, 1, qq);
+        rr[(g + PD) % XR] = OJX_SK_R(t, g + PD);
 #pragma unroll
         for (int qq = 0; qq < NS; ++qq) OJX_SK_MFMA(qq, g % NR, g < NR ? s0c[qq] : s1c[qq], rr[g % XR]);
         if constexpr (DPG > 0)
-          if (g < NDG) OJX_SK_DMA(bn, kn, H0 + g * DPG, min(GPW, H0 + (g + 1) * DPG));
+          if (g < NDG) OJX_SK_DMA(ta, H0 + g * DPG, min(GPW, H0 + (g + 1) * DPG));
       }
       sk_sched<0, NMG, NS, NR, DPG, NDG>();
       if (t + 1 < nk) {
-        // this wave's DMAs of stage t+1 have landed (three buffers: those of stage t+2, all issued, may not have)
-        wait_vmcnt<NBUF == 3 ? GPW : 0>();
+        // this wave's DMAs of stage t+1 have landed (three buffers: those of stage t+2, all issued, may not have;
+        // ASYM: the W of stage t+2 that batch t+1 issued last may not have)
+        wait_vmcnt<NBUF == 3 ? GPW : ASYM ? GW : 0>();
         dma_barrier();    // every wave's has, and every wave's reads of stage t are done
-        if constexpr (NBUF == 3) OJX_SK_DMA(bidx(t + 3), kb + (t + 3) * BK, 0, H0);  // unconditional: the count
-        else if (t + 2 < nk) OJX_SK_DMA(t & 1, kb + (t + 2) * BK, 0, H0);              // above relies on it
-        const uint8_t* sx = smem + bidx(t + 1) * STAGE;
+        if constexpr (NBUF == 3) OJX_SK_DMA(t + 3, 0, H0);  // unconditional: the count above relies on it
+        else if (t + 2 < nk) OJX_SK_DMA(t + 2, 0, H0);
 #pragma unroll
-        for (int qq = 0; qq < NS; ++qq) s0c[qq] = OJX_SK_S(sx, 0, qq);
+        for (int qq = 0; qq < NS; ++qq) s0c[qq] = OJX_SK_S(t + 1, 0, qq);
 #pragma unroll
-        for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(sx, d);
+        for (int d = 0; d < PD; ++d) rn[d] = OJX_SK_R(t + 1, d);
       }
 #pragma unroll
       for (int g = NGR - PD; g < NGR; ++g)
@@ -300,6 +327,8 @@ __device__ __forceinline__ void sk_body(const GemmParams& p) {
 #undef OJX_SK_R
 #undef OJX_SK_MFMA
 #undef OJX_SK_DMA
+#undef OJX_SK_DMAW
+#undef OJX_SK_SLOT
 
     // ------------------------------------------------------------------ partial tile: to its slot
     if (i0 != 0 || i1 != ipt) {
