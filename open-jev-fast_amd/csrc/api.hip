@@ -102,14 +102,16 @@ bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
   if (splitk < 1 || splitk > kMaxSplit) return false;
   if (is_sk(tile)) return true;  // splitk is the stream-K spread there, not a K split
   const int64_t ch = kchunk_for(K, splitk);
+  // the wave-split family (7) reads whole 64-k stages: every split boundary on a stage boundary
+  if (ojx::tile_info(tile)->family == 7 && (K % 64 != 0 || ch % 64 != 0)) return false;
   return (splitk - 1) * ch < K;  // every split owns a non-empty K range
 }
 
 // A packed weight is read by the K-interleaved family only, without tails, with splits of whole 64-k stages.
-// Tile families that read the packed layout: 0 (both operands through registers and LDS), 5 (persistent) and 6.
+// Tile families that read the packed layout: 0 (both operands through registers and LDS), 5 (persistent), 6 and 7.
 bool reads_packed(int32_t tile) {
   const ojx::TileInfo* t = ojx::tile_info(tile);
-  return t != nullptr && (t->family == 0 || t->family == 5 || t->family == 6);
+  return t != nullptr && (t->family == 0 || t->family == 5 || t->family == 6 || t->family == 7);
 }
 
 // A packed weight: no tails, splits of whole 64-k stages (the persistent family's splitk is its stream-K spread).

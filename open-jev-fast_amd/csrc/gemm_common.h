@@ -50,6 +50,17 @@ __device__ __forceinline__ u32x4 bload_asm_nt(const u32x4& r, uint32_t off) {  /
   asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(v) : "v"(off), "s"(r) : "memory");
   return v;
 }
+// The same loads with a wave-uniform byte offset in soffset (an SGPR) added to the lane's offset.
+__device__ __forceinline__ u32x4 bload_asm_s(const u32x4& r, uint32_t off, uint32_t soff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(off), "s"(r), "s"(soff) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x4 bload_asm_nt_s(const u32x4& r, uint32_t off, uint32_t soff) {
+  u32x4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(off), "s"(r), "s"(soff) : "memory");
+  return v;
+}
 // Same load into accumulation registers (AGPRs): used for data that only goes on to LDS, so the compiler never has
 // a reason to copy or spill it before the explicit wait (it cannot tell that the load is still in flight).
 __device__ __forceinline__ u32x4 bload_asm_agpr(const u32x4& r, uint32_t off) {
@@ -178,6 +189,11 @@ constexpr bool sk_asym(int BN, int BM) {
 constexpr int sk_lds(int BN, int BM) {
   return sk_asym(BN, BM) ? (3 * BN + 2 * BM) * 128 : sk_nbuf(BN, BM) * (BN + BM) * 128;
 }
+// Skinny weight streaming, K split over the waves of a workgroup (gemm_sw.hip): 16 FW W rows x 16 FM x rows.
+template <int FW, int FM, int NW, int D>
+__global__ void gemm_sw_kernel(const GemmParams p, const int epi);
+// Its dynamic LDS: one stage of (16 FW + 16 FM) rows x 128 B per wave (reused for the NW partial tiles).
+constexpr int sw_lds(int FW, int FM, int NW) { return NW * (16 * FW + 16 * FM) * 128; }
 // K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
 template <int FW, int FX, int XE>
 __global__ void gemm_kx_kernel(const GemmParams p, const int epi);
