@@ -13,7 +13,7 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB = os.path.join(HERE, "libojx.so")
-SOURCES = ["gemm.hip", "gemm_sk.hip", "gemm_kx.hip", "gemm_sw.hip", "epilogue.hip", "prep.hip", "api.hip"]
+SOURCES = ["gemm.hip", "gemm_sk.hip", "gemm_kx.hip", "epilogue.hip", "prep.hip", "api.hip"]
 OBJDIR = os.path.join(HERE, "_build")
 ARCH = "gfx950"
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

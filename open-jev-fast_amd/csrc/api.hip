@@ -102,16 +102,14 @@ bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
   if (splitk < 1 || splitk > kMaxSplit) return false;
   if (is_sk(tile)) return true;  // splitk is the stream-K spread there, not a K split
   const int64_t ch = kchunk_for(K, splitk);
-  // the wave-split family (7) reads whole 64-k stages: every split boundary on a stage boundary
-  if (ojx::tile_info(tile)->family == 7 && (K % 64 != 0 || ch % 64 != 0)) return false;
   return (splitk - 1) * ch < K;  // every split owns a non-empty K range
 }
 
-// A packed weight is read by the K-interleaved family only, without tails, with splits of whole 64-k stages.
-// Tile families that read the packed layout: 0 (both operands through registers and LDS), 5 (persistent), 6 and 7.
+// Tile families that read the packed layout (without tails, with splits of whole 64-k stages): 0 (both operands
+// through registers and LDS), 5 (persistent) and 6 (K-interleaved).
 bool reads_packed(int32_t tile) {
   const ojx::TileInfo* t = ojx::tile_info(tile);
-  return t != nullptr && (t->family == 0 || t->family == 5 || t->family == 6 || t->family == 7);
+  return t != nullptr && (t->family == 0 || t->family == 5 || t->family == 6);
 }
 
 // A packed weight: no tails, splits of whole 64-k stages (the persistent family's splitk is its stream-K spread).
@@ -650,8 +648,8 @@ int ojx_linattn_prep(const void* proj, const int32_t* hist, const int32_t* rep_p
   if (N < 0 || N >= (1LL << 31) - 1 || R < 0 || R >= (1LL << 31) || L2 < 1 || R % L2 != 0)
     return fail(OJX_ERR_SHAPE, "bad sizes N=%lld R=%lld L2=%lld (R a multiple of L2)", (long long)N, (long long)R,
                 (long long)L2);
-  if (N + (R + 15) / 16 > 65535) return fail(OJX_ERR_SHAPE, "N + R/16 = %lld rows of workgroups exceeds 65535",
-                                             (long long)(N + (R + 15) / 16));
+  if (2 * KD + VD > 28672)  // the finished row is held in LDS (2 bytes per conv channel)
+    return fail(OJX_ERR_SHAPE, "2 KD + VD = %d conv channels exceed 28672", 2 * KD + VD);
   if (R == 0) return OJX_OK;
   const void* ptrs[] = {proj, hist, rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta};
   for (const void* p : ptrs)
@@ -679,11 +677,16 @@ int ojx_gemm_residual_rmsnorm_noalloc(const void* x, const void* w, const void* 
     return fail(OJX_ERR_WORKSPACE, "config (tile %d, splitk %d) needs %lld bytes of workspace; the static scratch of "
                 "the allocation-free entry point holds %lld", c.tile, c.splitk, (long long)need,
                 (long long)kScratchBytes);
-  // The plan's own configuration, with its split-K count (or stream-K spread) lowered until its workspace fits.
-  while (need > kScratchBytes && c.splitk > 1) {
-    --c.splitk;
-    if (!cfg_fits(M, N, K, c)) continue;
-    need = workspace_for(c, M, N, K);
+  // The plan's own configuration, with its split-K count (or stream-K spread) lowered to the largest value that
+  // is valid for the shape and whose workspace fits; `need` always belongs to the configuration in `c`.
+  for (ojx_cfg t = c; need > kScratchBytes && t.splitk > 1;) {
+    --t.splitk;
+    if (!cfg_fits(M, N, K, t)) continue;
+    const int64_t nt = workspace_for(t, M, N, K);
+    if (nt <= kScratchBytes) {
+      c = t;
+      need = nt;
+    }
   }
   if (need > kScratchBytes)
     return fail(OJX_ERR_WORKSPACE, "M=%lld N=%lld K=%lld needs %lld bytes of workspace, more than the static scratch "

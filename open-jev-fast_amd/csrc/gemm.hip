@@ -827,10 +827,6 @@ struct TileEntry {
 #define OJX_WD(FN, FM, NW, D, BKX)                                                                           \
   {{NW * FN * 16, FM * 16, BKX, NW, 1, 64 * NW, 2 * (FM * 16) * (BKX + 8) * 2, 1}, gemm_wd_kernel<FN, FM, NW, D, BKX>}
 
-// Skinny weight-streaming tiles with the K split over the NW waves of the workgroup (gemm_sw.hip)
-#define OJX_SW(FW, FM, NW, D)                                                                                \
-  {{16 * FW, 16 * FM, 64, NW, 1, 64 * NW, sw_lds(FW, FM, NW), 7}, gemm_sw_kernel<FW, FM, NW, D>}
-
 // Order is the tile id used by the plan table; append only (ids are stored in plan_table.inc).
 static const TileEntry kTiles[] = {
     OJX_TILE(64, 16, 128, 4, 1),    // 0  skinny M, weight streaming
@@ -925,14 +921,6 @@ static const TileEntry kTiles[] = {
     OJX_KX(16, 1, 0),               // 89 256 x 64
     OJX_TILE(32, 16, 128, 2, 1),    // 90 skinny M, 32 W rows: N / 32 workgroups without split-K
     OJX_TILE(32, 16, 256, 2, 1),    // 91 the same, deeper K stages
-    OJX_SW(1, 1, 8, 4),             // 92 16 W rows x 16, K over 8 waves: N / 16 workgroups, one launch
-    OJX_SW(1, 1, 16, 4),            // 93 16 x 16, K over 16 waves
-    OJX_SW(2, 1, 8, 4),             // 94 32 x 16
-    OJX_SW(2, 1, 16, 3),            // 95 32 x 16, 16 waves
-    OJX_SW(4, 1, 8, 3),             // 96 64 x 16
-    OJX_SW(1, 2, 16, 3),            // 97 16 x 32, 16 waves
-    OJX_SW(2, 2, 8, 3),             // 98 32 x 32
-    OJX_SW(1, 1, 4, 6),             // 99 16 x 16, K over 4 waves, 6 stages in flight
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

@@ -189,11 +189,6 @@ constexpr bool sk_asym(int BN, int BM) {
 constexpr int sk_lds(int BN, int BM) {
   return sk_asym(BN, BM) ? (3 * BN + 2 * BM) * 128 : sk_nbuf(BN, BM) * (BN + BM) * 128;
 }
-// Skinny weight streaming, K split over the waves of a workgroup (gemm_sw.hip): 16 FW W rows x 16 FM x rows.
-template <int FW, int FM, int NW, int D>
-__global__ void gemm_sw_kernel(const GemmParams p, const int epi);
-// Its dynamic LDS: one stage of (16 FW + 16 FM) rows x 128 B per wave (reused for the NW partial tiles).
-constexpr int sw_lds(int FW, int FM, int NW) { return NW * (16 * FW + 16 * FM) * 128; }
 // K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
 template <int FW, int FX, int XE>
 __global__ void gemm_kx_kernel(const GemmParams p, const int epi);

@@ -1,130 +1,154 @@
-// Full-attention prep: the consumer of the full-attention layers' in-projection output.
-//
-// Reference: fullattn_prep2_k (src/kernels.cu:302-355), called from forward_gtree as
-// K.fullattn_prep2(proj, qw1, kw1, cos, sin, 1, N, HQ, HKV, D, eps) (src/fastmodel.py:462). proj [N, P] bf16 with
-// P = HQ 2D + 2 HKV D; per token n and head:
-//   q head h: x = proj[n][2hD .. 2hD+D), gate head h = proj[n][2hD+D .. 2hD+2D);
-//   k head h: x = proj[n][2 HQ D + hD ..); v head h = proj[n][2 HQ D + HKV D + hD ..).
-//   q and k: xn = bf16((x * rsqrt(sum x^2 / D + eps)) * w1[d]) with w1 = qw1 / kw1 [D] fp32, then on the first RD
-//   dims the rotate-half RoPE: out = bf16(bf16(xn * cos[n][d]) + bf16(rh * sin[n][d])), rh = -xn[d + RD/2] for
-//   d < RD/2 and xn[d - RD/2] for RD/2 <= d < RD; dims >= RD keep xn.
-//   Outputs (B = 1, T = N): qt [HQ, N, D], kt [HKV, N, D], vt [HKV, N, D] (head-major for attention) and
-//   gate [N, HQ D].
-//
-// Two (token, head task) pairs per wave64, 32 lanes each with 8 consecutive dims (one 16-byte load and store per
-// lane, D = 256): the row's sum of squares is a butterfly over the 32 lanes, and the RoPE partner of lane l is lane
-// l ^ (RD / 16), because dims d and d +- RD/2 sit RD/16 lanes apart and RD/16 is a power of two below 32
-// (RD = 16 .. 256).
+// The two consumers of the in-projection output that forward_gtree calls by default: the full-attention prep and
+// the linear-attention prep on the tree layout. Both are one workgroup per token row: the row is read once,
+// finished in LDS, and written out with whole 8- or 16-byte vector stores.
 #include "ojx_internal.h"
 
 namespace ojx {
 
 namespace {
 
-__device__ __forceinline__ void unpack8(uint4 a, float (&v)[8]) {
-  const uint32_t w[4] = {a.x, a.y, a.z, a.w};
+// Sum over the 64 lanes of a wave (every lane gets the total).
+__device__ __forceinline__ float wave_total(float v) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = bf2f(w[i] & 0xffffu);
-    v[2 * i + 1] = bf2f(w[i] >> 16);
-  }
+  for (int o = 1; o < 64; o <<= 1) v += __shfl_xor(v, o);
+  return v;
+}
+
+__device__ __forceinline__ void unpack4(uint2 a, float (&v)[4]) {
+  v[0] = bf2f(a.x & 0xffffu);
+  v[1] = bf2f(a.x >> 16);
+  v[2] = bf2f(a.y & 0xffffu);
+  v[3] = bf2f(a.y >> 16);
 }
 
 }  // namespace
 
+// ------------------------------------------------------------------------------------------------ full attention
+// Reference behaviour: fullattn_prep2 (src/kernels.cu:302-355), called from forward_gtree as
+// K.fullattn_prep2(proj, qw1, kw1, cos, sin, 1, N, HQ, HKV, D, eps) (src/fastmodel.py:462). proj [N, P] bf16 with
+// P = HQ 2D + 2 HKV D; for token n:
+//   q head h: x = proj[n][2hD .. 2hD+D), gate head h = proj[n][2hD+D .. 2hD+2D);
+//   k head h: x = proj[n][2 HQ D + hD ..); v head h = proj[n][2 HQ D + HKV D + hD ..).
+//   q and k: xn = bf16((x * rsqrt(sum x^2 / D + eps)) * w1[d]) with w1 = qw1 / kw1 [D] fp32, then on the first RD
+//   dims the rotate-half RoPE: out = bf16(bf16(xn * cos[n][d]) + bf16(rh * sin[n][d])), rh = -xn[d + RD/2] for
+//   d < RD/2 and xn[d - RD/2] for RD/2 <= d < RD; dims >= RD keep xn.
+//   Outputs: qt [HQ, N, D], kt [HKV, N, D], vt [HKV, N, D] (head-major for attention) and gate [N, HQ D].
+//
+// Work layout: one workgroup of four waves per token. The gate and v parts are pure copies, done first by all 256
+// lanes as 16-byte moves. The HQ + HKV normalised heads are then taken in rounds of four, one head per wave, with
+// lane l owning dims 4l .. 4l+3 (one 8-byte load, one 8-byte store, 512 contiguous bytes per wave). The head's
+// sum of squares is a 64-lane wave total. The normalised head goes to the wave's 1 KB LDS row, from which each
+// lane of the rotary part reads the four partner values xn[d -+ RD/2] after a workgroup barrier.
 __global__ void __launch_bounds__(256) fullattn_prep_k(const uint16_t* __restrict__ proj, int64_t N, int HQ, int HKV,
                                                        int RD, float eps, const float* __restrict__ qw1,
                                                        const float* __restrict__ kw1, const uint16_t* __restrict__ cosb,
                                                        const uint16_t* __restrict__ sinb, uint16_t* __restrict__ qt,
                                                        uint16_t* __restrict__ kt, uint16_t* __restrict__ vt,
                                                        uint16_t* __restrict__ gate) {
-  constexpr int D = 256;
-  const int lane = threadIdx.x & 31;
-  const int ntask = HQ + 2 * HKV;
-  const int64_t wid = (int64_t)blockIdx.x * (blockDim.x >> 5) + (threadIdx.x >> 5);
-  if (wid >= N * ntask) return;  // whole 32-lane halves leave together
-  const int64_t n = wid / ntask;
-  const int task = (int)(wid - n * ntask);
+  constexpr int D = 256, CH = D / 8;  // 16-byte chunks per head
+  __shared__ float4 xn_lds[4][D / 4];
+  const int64_t n = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int64_t P = (int64_t)(2 * HQ + 2 * HKV) * D;
   const uint16_t* row = proj + n * P;
-  const int d0 = lane * 8;
-  if (task >= HQ + HKV) {  // v head: a copy into [HKV, N, D]
-    const int h = task - HQ - HKV;
-    *reinterpret_cast<uint4*>(vt + ((int64_t)h * N + n) * D + d0) =
-        *reinterpret_cast<const uint4*>(row + 2 * HQ * D + HKV * D + h * D + d0);
-    return;
+
+  // copies: gate heads (HQ x CH chunks), then v heads (HKV x CH chunks)
+  for (int i = tid; i < (HQ + HKV) * CH; i += 256) {
+    const int h = i / CH, c = (i - h * CH) * 8;
+    if (h < HQ) {
+      *reinterpret_cast<uint4*>(gate + n * (int64_t)(HQ * D) + h * D + c) =
+          *reinterpret_cast<const uint4*>(row + (int64_t)h * 2 * D + D + c);
+    } else {
+      const int hv = h - HQ;
+      *reinterpret_cast<uint4*>(vt + ((int64_t)hv * N + n) * D + c) =
+          *reinterpret_cast<const uint4*>(row + (int64_t)(2 * HQ + HKV) * D + hv * D + c);
+    }
   }
-  const bool isq = task < HQ;
-  const int h = isq ? task : task - HQ;
-  if (isq)  // gate head: a copy into [N, HQ D]
-    *reinterpret_cast<uint4*>(gate + n * (int64_t)(HQ * D) + h * D + d0) =
-        *reinterpret_cast<const uint4*>(row + (int64_t)h * 2 * D + D + d0);
-  float x[8];
-  unpack8(*reinterpret_cast<const uint4*>(row + (isq ? (int64_t)h * 2 * D : 2 * HQ * D + (int64_t)h * D) + d0), x);
-  float ss = 0.f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) ss += x[j] * x[j];
-#pragma unroll
-  for (int o = 16; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
-  const float r = rsqrtf(ss / (float)D + eps);
-  const float* w1 = (isq ? qw1 : kw1) + d0;
-  const float4 wa = *reinterpret_cast<const float4*>(w1), wb = *reinterpret_cast<const float4*>(w1 + 4);
-  const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-  float nv[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) nv[j] = rbf((x[j] * r) * wv[j]);
-  const int hl = RD >> 4;  // partner lane distance
-  float pv[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) pv[j] = __shfl_xor(nv[j], hl);
-  float out[8];
-  if (d0 < RD) {
-    float c[8], sn[8];
-    unpack8(*reinterpret_cast<const uint4*>(cosb + n * RD + d0), c);
-    unpack8(*reinterpret_cast<const uint4*>(sinb + n * RD + d0), sn);
-    const bool lo = d0 < RD / 2;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) out[j] = rbf(rbf(nv[j] * c[j]) + rbf((lo ? -pv[j] : pv[j]) * sn[j]));
-  } else {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) out[j] = nv[j];
+
+  const int d0 = lane * 4;
+  const bool rot = d0 < RD;
+  float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
+  if (rot) {
+    unpack4(*reinterpret_cast<const uint2*>(cosb + n * RD + d0), cs);
+    unpack4(*reinterpret_cast<const uint2*>(sinb + n * RD + d0), sn);
   }
-  uint16_t* dst = isq ? qt : kt;
-  *reinterpret_cast<uint4*>(dst + ((int64_t)h * N + n) * D + d0) =
-      make_uint4(pack2(out[0], out[1]), pack2(out[2], out[3]), pack2(out[4], out[5]), pack2(out[6], out[7]));
+  const int pd = d0 < RD / 2 ? d0 + RD / 2 : d0 - RD / 2;  // partner dims (used on the rotary part only)
+  const float sgn = d0 < RD / 2 ? -1.f : 1.f;
+  const int T = HQ + HKV;
+  for (int base = 0; base < T; base += 4) {  // uniform trip count: every wave meets every barrier
+    const int t = base + wave;
+    const bool live = t < T;
+    const bool isq = t < HQ;
+    float xn[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) {
+      const uint16_t* src = row + (isq ? (int64_t)t * 2 * D : (int64_t)2 * HQ * D + (int64_t)(t - HQ) * D) + d0;
+      float x[4];
+      unpack4(*reinterpret_cast<const uint2*>(src), x);
+      float ss = x[0] * x[0];
+      ss += x[1] * x[1];
+      ss += x[2] * x[2];
+      ss += x[3] * x[3];
+      const float r = rsqrtf(wave_total(ss) / (float)D + eps);
+      const float4 w = *reinterpret_cast<const float4*>((isq ? qw1 : kw1) + d0);
+      xn[0] = rbf((x[0] * r) * w.x);
+      xn[1] = rbf((x[1] * r) * w.y);
+      xn[2] = rbf((x[2] * r) * w.z);
+      xn[3] = rbf((x[3] * r) * w.w);
+      xn_lds[wave][lane] = make_float4(xn[0], xn[1], xn[2], xn[3]);
+    }
+    __syncthreads();
+    if (live) {
+      float o[4] = {xn[0], xn[1], xn[2], xn[3]};
+      if (rot) {
+        const float4 p = xn_lds[wave][pd >> 2];
+        const float pv[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = rbf(rbf(xn[j] * cs[j]) + rbf((sgn * pv[j]) * sn[j]));
+      }
+      uint16_t* dst = isq ? qt + ((int64_t)t * N + n) * D : kt + ((int64_t)(t - HQ) * N + n) * D;
+      *reinterpret_cast<uint2*>(dst + d0) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+    }
+    __syncthreads();  // the LDS row is rewritten by the next round
+  }
 }
 
 hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV, int RD, float eps,
                                 const float* qw1, const float* kw1, const uint16_t* cosb, const uint16_t* sinb,
                                 uint16_t* qt, uint16_t* kt, uint16_t* vt, uint16_t* gate, hipStream_t st) {
-  const int64_t halves = N * (HQ + 2 * HKV);
-  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)((halves + 7) / 8)), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps,
-                     qw1, kw1, cosb, sinb, qt, kt, vt, gate);
+  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)N), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps, qw1, kw1, cosb,
+                     sinb, qt, kt, vt, gate);
   return hipGetLastError();
 }
 
-// Linear-attention prep on the tree layout: the consumer of the linear-attention layers' in-projection.
-//
-// Reference: linattn_prep_dedup2_k (src/kernels.cu:1176-1265), called from forward_gtree as
+// ------------------------------------------------------------------------------------------------ linear attention
+// Reference behaviour: linattn_prep_dedup2 (src/kernels.cu:1176-1265), called from forward_gtree as
 // K.linattn_prep_dedup2(proj, lay.hist, lay.rep_ptr, lay.rep_pos, lay.L2, convw, A_log, dt_bias, KD, VD, HV, HK, HD,
 // rep_qk) (src/fastmodel.py:420,438). proj [N, P] bf16, P = C + VD + 2 HV with C = 2 KD + VD conv channels
 // (q | k | v), then the z gate (VD, read later by the gated norm), then b [HV] and a [HV]. Each packed row n is
 // computed once and written to every slot s = rep_pos[p], p in [rep_ptr[n], rep_ptr[n+1]) (the candidate paths that
 // contain it); the slots of group N (rep_ptr[N] .. rep_ptr[N+1]) are the paths' end padding and receive zeros.
-//   channel c: conv = sum_{i=0..3} convw[c][i] * proj[hist[n][i]][c] in that order (hist[n] = the rows t-3 .. t on
-//   the row's path, -1 = none), o = bf16(silu(conv)); q and k channels (c < 2 KD) are then L2-normalised over their
-//   head of HD = 128 channels: o * (1 / sqrt(sum o^2 + 1e-6)), the sum added by a butterfly over 16 lanes of 8
-//   channels each (xor 8, 4, 2, 1, each lane's 8 squares added in order first), and rounded to bf16.
+//   channel c: conv = sum_{i=0..3} convw[c][i] * proj[hist[n][i]][c], added in that order (hist[n] = the rows
+//   t-3 .. t on the row's path, -1 = none); o = bf16(silu(conv)). q and k channels (c < 2 KD) are then
+//   L2-normalised over their head of HD = 128 channels: bf16(o * (1 / sqrt(sum o^2 + 1e-6))).
 //   head h < HV: beta = bf16(sigmoid(b_h)), g = -exp(A_log[h]) * softplus(a_h + dt_bias[h]) (fp32, softplus(x) = x
-//   above 20).
-//   Outputs: q, k [R, RQ HK HD] (RQ = 1, or 3 = HV / HK copies of each head side by side), v [R, VD], g [R, HV] fp32,
+//   above 20), b and a read from row hist[n][3].
+//   Outputs: q, k [R, HK RQ HD] (RQ = 1, or 3 = HV / HK copies of each head side by side), v [R, VD], g [R, HV] fp32,
 //   beta [R, HV] bf16; R = rep_pos's length.
+// Products of two bf16 values are exact in fp32, so the conv's sum order is the only one that fixes its bits; it is
+// kept. The head sums of squares are added in another order than the reference's (one rounding step at most).
 //
-// Layout of the work: a workgroup of 256 lanes takes 2048 channels of one packed row (each lane 8 consecutive
-// channels, one 16-byte load per history row, 16 lanes = one q/k head), computes them once and stores them to each of
-// the row's slots (a wave writes 1 KB contiguous per slot). Workgroups past the N packed rows write the
-// end-padding slots, 16 slots each. Products of two bf16 values are exact in fp32, so the conv's sum is the only rounding order that
-// matters, and it is kept.
+// Work layout: one workgroup of four waves per packed row, grid = N rows + the padding groups.
+//   1. conv + SiLU for all C channels (8 per lane per step, the four history rows and the 64 weight bytes as 16-byte
+//      loads), the bf16 results kept in an LDS copy of the row;
+//   2. one q/k head per wave at a time, 2 channels per lane: wave-total sum of squares, scaled in place in LDS;
+//      lanes below HV compute the gates into LDS meanwhile;
+//   3. the finished row is written slot after slot: every 16-byte chunk of a slot's q | k | v row is one lane's
+//      LDS read and global store, so each slot row goes out as one contiguous sweep; slot ids come in through
+//      LDS, 256 at a time.
+// A padding group (the workgroups after the N row workgroups) writes zero rows to kPadSlots consecutive
+// padding slots.
+constexpr int kPadSlots = 32;
+
 template <int RQ>
 __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict__ proj, const int4* __restrict__ hist,
                                                      const int* __restrict__ rep_ptr, const int* __restrict__ rep_pos,
@@ -135,103 +159,113 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
                                                      float* __restrict__ g, uint16_t* __restrict__ beta, int N, int KD,
                                                      int VD, int HV) {
   constexpr int HD = 128;
+  extern __shared__ uint4 lds_raw[];
   const int C = 2 * KD + VD;
   const int64_t P = (int64_t)C + VD + 2 * HV;
-  // plain row-major numbering: an XCD-contiguous run of rows was measured slower (the prompt rows, written to
-  // every path, then pile onto one XCD)
-  const int n = blockIdx.y, bx = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = blockIdx.x;
   const bool pad = n >= N;
   int p0, p1;
   if (!pad) {
     p0 = rep_ptr[n];
     p1 = rep_ptr[n + 1];
   } else {
-    p0 = rep_ptr[N] + (n - N) * 16;
-    p1 = min(rep_ptr[N + 1], p0 + 16);
+    p0 = rep_ptr[N] + (n - N) * kPadSlots;
+    p1 = min(rep_ptr[N + 1], p0 + kPadSlots);
   }
-  if (p0 >= p1) return;
-  const int4 hr = pad ? make_int4(-1, -1, -1, -1) : hist[n];
-  const int tid = threadIdx.x;
-  const bool gate_lane = bx == 0 && tid < HV;  // per-head gates
-  float bv = 0.f, gv = 0.f;
-  if (gate_lane && !pad) {
-    const uint16_t* row = proj + (int64_t)hr.w * P + C + VD;
-    bv = sigmoid_f(bf2f(row[tid]));
-    const float xs = bf2f(row[HV + tid]) + bf2f(dt_bias[tid]);
-    gv = -expf(bf2f(A_log[tid])) * (xs > 20.f ? xs : log1pf(expf(xs)));
-  }
-  const uint16_t bb = (uint16_t)f2bf(bv);
-  const int c0 = (bx * 256 + tid) * 8;
-  const bool live = c0 < C;  // C is a multiple of 128: a 16-lane head group is either all in or all out
-  const bool isqk = c0 < 2 * KD;
-  uint4 ov = make_uint4(0u, 0u, 0u, 0u);
-  if (live && !pad) {
+  if (p0 >= p1) return;  // uniform over the workgroup
+
+  uint16_t* orow = reinterpret_cast<uint16_t*>(lds_raw);                 // [C] bf16 bits
+  float* gl = reinterpret_cast<float*>(orow + C);                         // [HV] g
+  uint16_t* bl = reinterpret_cast<uint16_t*>(gl + HV);                    // [HV] beta bits
+  int* slot = reinterpret_cast<int*>(lds_raw) + (C * 2 + HV * 6 + 15) / 16 * 4;  // [256] slot ids
+
+  if (!pad) {
+    const int4 hr = hist[n];
     const int rows[4] = {hr.x, hr.y, hr.z, hr.w};
-    uint4 xr[4];
+    for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
+      uint4 xr[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      xr[i] = rows[i] >= 0 ? *reinterpret_cast<const uint4*>(proj + (int64_t)rows[i] * P + c0) : make_uint4(0, 0, 0, 0);
-    uint4 wr[4];  // convw[c0 .. c0+8)[0..4): 64 contiguous bytes
+      for (int i = 0; i < 4; ++i)
+        xr[i] = rows[i] >= 0 ? *reinterpret_cast<const uint4*>(proj + (int64_t)rows[i] * P + c0)
+                             : make_uint4(0u, 0u, 0u, 0u);
+      const uint4* wp = reinterpret_cast<const uint4*>(convw + (int64_t)c0 * 4);  // [8 channels][4 taps]
+      const uint4 wq[4] = {wp[0], wp[1], wp[2], wp[3]};
+      const uint32_t* wv = &wq[0].x;
+      uint32_t packed[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) wr[u] = *reinterpret_cast<const uint4*>(convw + (int64_t)c0 * 4 + u * 8);
-    const uint32_t* xw[4] = {&xr[0].x, &xr[1].x, &xr[2].x, &xr[3].x};
-    const uint32_t* ww = &wr[0].x;
-    float o[8];
+      for (int j = 0; j < 8; j += 2) {
+        float o2[2];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float acc = 0.f;
+        for (int jj = 0; jj < 2; ++jj) {
+          const int ch = j + jj;
+          float acc = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t xb = (xw[i][j >> 1] >> ((j & 1) * 16)) & 0xffffu;
-        const uint32_t wb = (ww[(j * 4 + i) >> 1] >> (((j * 4 + i) & 1) * 16)) & 0xffffu;
-        acc += bf2f(wb) * bf2f(xb);
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t* xw = &xr[i].x;
+            const float xv = bf2f((xw[ch >> 1] >> ((ch & 1) * 16)) & 0xffffu);
+            const int wi = ch * 4 + i;
+            const float wf = bf2f((wv[wi >> 1] >> ((wi & 1) * 16)) & 0xffffu);
+            acc += wf * xv;
+          }
+          o2[jj] = silu_f(acc);
+        }
+        packed[j >> 1] = pack2(o2[0], o2[1]);
       }
-      o[j] = rbf(silu_f(acc));
+      *reinterpret_cast<uint4*>(orow + c0) = make_uint4(packed[0], packed[1], packed[2], packed[3]);
     }
-    if (isqk) {
-      float ss = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) ss += o[j] * o[j];
-#pragma unroll
-      for (int off = 8; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
-      const float rs = 1.0f / sqrtf(ss + 1e-6f);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = o[j] * rs;
+    if (tid < HV) {
+      const uint16_t* br = proj + (int64_t)hr.w * P + C + VD;
+      bl[tid] = (uint16_t)f2bf(sigmoid_f(bf2f(br[tid])));
+      const float xs = bf2f(br[HV + tid]) + bf2f(dt_bias[tid]);
+      gl[tid] = -expf(bf2f(A_log[tid])) * (xs > 20.f ? xs : log1pf(expf(xs)));
     }
-    ov = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+    __syncthreads();
+    // q / k heads: one per wave at a time, channels 2 lane, 2 lane + 1
+    for (int h = wave; h < 2 * KD / HD; h += 4) {
+      uint32_t* pr = reinterpret_cast<uint32_t*>(orow + h * HD) + lane;
+      const uint32_t u = *pr;
+      const float a = bf2f(u & 0xffffu), b = bf2f(u >> 16);
+      float ss = a * a;
+      ss += b * b;
+      const float rs = 1.0f / sqrtf(wave_total(ss) + 1e-6f);
+      *pr = pack2(a * rs, b * rs);
+    }
   }
-  // destination of this lane's 8 channels within a slot's row
-  uint16_t* dst;
-  int64_t rowlen;
-  if (isqk) {
-    const int cc = c0 < KD ? c0 : c0 - KD;
-    const int hk = cc / HD;
-    dst = (c0 < KD ? q : k) + (int64_t)hk * RQ * HD + (cc - hk * HD);
-    rowlen = (int64_t)RQ * KD;
-  } else {
-    dst = v + (c0 - 2 * KD);
-    rowlen = VD;
-  }
-  // The row's slots, staged through LDS 256 at a time: one coalesced load, then every lane reads the slot ids as
-  // LDS broadcasts (independent reads the compiler can issue ahead, instead of a chain of dependent scalar loads).
-  __shared__ int slot[256];
+  __syncthreads();
+
+  // scatter: chunk u of a slot row is q (u < QC), k (QC <= u < 2 QC) or v; q/k rows hold each head RQ times
+  const int QC = RQ * KD / 8, VC = VD / 8, U = 2 * QC + VC;
   for (int base = p0; base < p1; base += 256) {
     const int cnt = min(256, p1 - base);
     if (tid < cnt) slot[tid] = rep_pos[base + tid];
     __syncthreads();
-    if (gate_lane)
-      for (int j = 0; j < cnt; ++j) {
-        const int64_t sp = slot[j];
-        beta[sp * HV + tid] = bb;
-        g[sp * HV + tid] = gv;
+    for (int j = 0; j < cnt; ++j) {
+      const int64_t s = slot[j];
+      for (int u = tid; u < U; u += 256) {
+        uint4 val = make_uint4(0u, 0u, 0u, 0u);
+        uint16_t* dst;
+        int src;
+        if (u < 2 * QC) {
+          const bool isk = u >= QC;
+          const int e = (u - (isk ? QC : 0)) * 8;  // element within the RQ KD row
+          const int hk = e / (RQ * HD);
+          src = (isk ? KD : 0) + hk * HD + (e - hk * RQ * HD) % HD;
+          dst = (isk ? k : q) + s * (int64_t)(RQ * KD) + e;
+        } else {
+          const int e = (u - 2 * QC) * 8;
+          src = 2 * KD + e;
+          dst = v + s * (int64_t)VD + e;
+        }
+        if (!pad) val = *reinterpret_cast<const uint4*>(orow + src);
+        *reinterpret_cast<uint4*>(dst) = val;
       }
-    if (live)
-      for (int j = 0; j < cnt; ++j) {
-        uint16_t* o = dst + (int64_t)slot[j] * rowlen;
-#pragma unroll
-        for (int r = 0; r < (isqk ? RQ : 1); ++r) *reinterpret_cast<uint4*>(o + r * HD) = ov;
+      if (tid < HV) {
+        g[s * HV + tid] = pad ? 0.f : gl[tid];
+        beta[s * HV + tid] = pad ? (uint16_t)0 : bl[tid];
       }
-    __syncthreads();
+    }
+    __syncthreads();  // slot[] is refilled by the next batch
   }
 }
 
@@ -240,13 +274,14 @@ hipError_t launch_linattn_prep(const uint16_t* proj, const int32_t* hist, const 
                                const uint16_t* A_log, const uint16_t* dt_bias, int KD, int VD, int HV, int RQ,
                                uint16_t* q, uint16_t* k, uint16_t* v, float* g, uint16_t* beta, hipStream_t st) {
   const int C = 2 * KD + VD;
-  const dim3 grid((unsigned)((C / 8 + 255) / 256), (unsigned)(N + (R + 15) / 16));
+  const size_t lds = (size_t)((C * 2 + HV * 6 + 15) / 16) * 16 + 256 * sizeof(int);
+  const dim3 grid((unsigned)(N + (R + kPadSlots - 1) / kPadSlots));
   if (RQ == 3)
-    hipLaunchKernelGGL(linattn_prep_k<3>, grid, dim3(256), 0, st, proj, reinterpret_cast<const int4*>(hist), rep_ptr,
-                       rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
+    hipLaunchKernelGGL(linattn_prep_k<3>, grid, dim3(256), lds, st, proj, reinterpret_cast<const int4*>(hist),
+                       rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
   else
-    hipLaunchKernelGGL(linattn_prep_k<1>, grid, dim3(256), 0, st, proj, reinterpret_cast<const int4*>(hist), rep_ptr,
-                       rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
+    hipLaunchKernelGGL(linattn_prep_k<1>, grid, dim3(256), lds, st, proj, reinterpret_cast<const int4*>(hist),
+                       rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
   return hipGetLastError();
 }
 

@@ -59,9 +59,11 @@ def _workspace(M, N, K, kind, cfg, device):
     """Workspace of one call: split-K fp32 planes or stream-K partial tiles (scratch, contents irrelevant on entry).
 
     One buffer per device is kept and grown as needed. A graph capture records the buffer's address, so a buffer
-    that a capture has used is never freed: when an eager call later needs a larger one, the old buffer moves to
-    _WS_KEEP instead of going back to the caching allocator (where a replay would write into memory that other
-    tensors may own by then). A capture that needs more than the kept buffer gets a buffer of its own, also kept.
+    that a capture has used is not freed while graphs may replay: when a later call needs a larger one, the old
+    buffer moves to _WS_KEEP instead of going back to the caching allocator (where a replay would write into memory
+    that other tensors may own by then). The larger buffer becomes the device's buffer for every later call,
+    eager or captured, so the kept memory grows only with the largest workspace seen, not with the number of
+    captures. release_workspaces() drops the kept buffers once the caller's graphs are gone.
     Calls that run concurrently on different streams of one device would share the buffer: such callers pass a
     workspace of their own through the C-ABI."""
     n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
@@ -77,13 +79,19 @@ def _workspace(M, N, K, kind, cfg, device):
             _WS[key] = ws = (ws[0], True)
             _WS_KEEP.append(ws[0])
         return ws[0], ws[0].numel()
-    if capturing:
-        buf = torch.empty(n, dtype=torch.uint8, device=device)
-        _WS_KEEP.append(buf)
-        return buf, n
     buf = torch.empty(max(n, 1 << 20), dtype=torch.uint8, device=device)
-    _WS[key] = (buf, False)   # the old buffer, if a capture used it, stays alive in _WS_KEEP
+    _WS[key] = (buf, capturing)   # the old buffer, if a capture used it, stays alive in _WS_KEEP
+    if capturing:
+        _WS_KEEP.append(buf)
     return buf, buf.numel()
+
+
+def release_workspaces():
+    """Frees the workspace buffers kept for captured graphs (and the current ones). Call it only after every graph
+    captured with this module's calls has been destroyed: a later replay of such a graph would write into freed
+    memory."""
+    _WS.clear()
+    _WS_KEEP.clear()
 
 
 def _chk_norm(w1, rowmask, M, H):

@@ -27,7 +27,7 @@ def _assert_tol(O, out, ref, what):
 
 def _packed_tiles(pkg):
     L = pkg._lib
-    return [t for t in range(L.lib().ojx_num_tiles()) if L.tile_info(t)["family"] in (0, 5, 6, 7)]
+    return [t for t in range(L.lib().ojx_num_tiles()) if L.tile_info(t)["family"] in (0, 5, 6)]
 
 
 def test_pack_weight_layout(ext, O, dev):

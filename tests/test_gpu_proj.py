@@ -38,10 +38,6 @@ def test_mm_every_tile_vs_oracle(pkg, ext, O, dev, M, N, K):
     for t in _tiles(pkg):
         for S in (1, 3):
             _say(f"case mm M={M} N={N} K={K} tile={t} S={S}")
-            if pkg._lib.tile_info(t)["family"] == 7 and (K % 64 or -(-(-(-K // S)) // 8) * 8 % 64):
-                with pytest.raises(RuntimeError, match="invalid"):  # the wave-split family needs whole 64-k stages
-                    ext.mm(xd, wd, cfg=(t, S))
-                continue
             y = ext.mm(xd, wd, cfg=(t, S))
             _assert_tol(O, y, ref, f"tile {t} S {S}")
 
@@ -60,8 +56,7 @@ def test_mm_planned_and_f64(pkg, ext, O, dev, M, N, K):
 def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
     """Without split-K the tiles of one MFMA shape sum K in the same order: outputs are bit-identical across those
     tiles and across runs (16x16x32 families 0-2 and 5; the 32x32x16 families 3-4 among themselves; the
-    K-interleaved family 6, which adds the sums of the even and odd 32-k blocks, among itself; the wave-split
-    family 7, which sums one partial per wave, among the tiles with the same wave count)."""
+    K-interleaved family 6, which adds the sums of the even and odd 32-k blocks, among itself)."""
     M, N, K = 96, 512, 1024
     x, w = O.seeded_inputs(M, N, K, seed=3)
     xd, wd = x.to(dev), w.to(dev)
@@ -69,14 +64,13 @@ def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
     base = {}
     for t in _tiles(pkg):
         fam = pkg._lib.tile_info(t)["family"]
-        info = pkg._lib.tile_info(t)
-        shape = 32 if fam in (3, 4) else "kx" if fam == 6 else ("sw", info["wn"]) if fam == 7 else 16
+        shape = 32 if fam in (3, 4) else "kx" if fam == 6 else 16
         y = ext.mm(xd, wd, cfg=(t, 1))
         if shape not in base:
             base[shape] = y
         assert torch.equal(y, base[shape]), f"tile {t}"
         assert torch.equal(y, ext.mm(xd, wd, cfg=(t, 1))), f"tile {t} not deterministic"
-    assert len([k for k in base if not isinstance(k, tuple)]) == 3 and len(base) > 3
+    assert len(base) == 3
     for S in (2, 4):
         a = ext.mm(xd, wd, cfg=(6, S))
         assert torch.equal(a, ext.mm(xd, wd, cfg=(6, S))), "split-K not deterministic"
