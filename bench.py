@@ -8,7 +8,8 @@ copies (712 MB), more than the 256 MB Infinity Cache, so every step streams its 
 
 Prints ONE JSON line with the metric, the roofline of the dominant kernel (HIP events on the launch stream), the
 CPU baseline (the oracle's torch CPU path on a bounded sample of the same workload, on this host's cores) and the
-per-shape table at M = 7 / 64 / 288 / 539 / 2048 for the five projection shapes.
+per-shape table at M = 7 / 64 / 288 / 539 / 2048 for the five projection shapes, and the BASELINE configs[4]
+64-layer projection stack at M = 539 (`stack_ms`, `stack_frac`: one graph replay per forward, packed weights).
 
 Other modes (each prints its own JSON lines): --sweep (full M sweep, every shape), --stack (
 the 64-layer projection stack at M = 539 in one graph replay), --head (the scoring head GEMV), --vs-hipblaslt
@@ -208,6 +209,7 @@ def main_default(args, pkg, ext, perf):
             for m in SHAPE_MS:
                 rr = measure_shape(ext, perf, name, m)
                 shapes[f"{name}_M{m}"] = {k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}
+    stack = None if args.no_stack else run_stack(ext, perf, 5)
     cpu = None if args.no_cpu else cpu_baseline(M, I, K)
     line = {
         "metric": METRIC, "value": round(r["tflops"], 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -223,6 +225,9 @@ def main_default(args, pkg, ext, perf):
                                 "tail_splitk": plan.tail_splitk} if plan.tail_rows else {})}},
         "gbs": round(r["gbs"], 1), "roofline_frac": round(r["frac"], 4),
         "roofline": roof, "cpu_baseline": cpu, "shapes": shapes,
+        # BASELINE configs[4] beside the headline: the whole 64-layer projection forward at M = 539
+        "stack_ms": None if stack is None else stack["ms"], "stack_frac": None if stack is None else stack["frac"],
+        "stack": stack,
     }
     print(json.dumps(line), flush=True)
 
@@ -252,11 +257,12 @@ def main_sweep(args, pkg, ext, perf):
                               **{k: round(v, 4) if isinstance(v, float) else v for k, v in rr.items()}}), flush=True)
 
 
-def main_stack(args, pkg, ext, perf):
+def run_stack(ext, perf, reps):
     """48 linear-attention + 16 full-attention layers, hidden 5120, MLP 17408, M = 539.
     Each layer: in-proj, out-proj + residual + RMSNorm, gate-up + SiLU.mul, down + residual + RMSNorm, back to
-    back in one graph. The attention cores between in-proj and out-proj are out of scope: the out-proj reads a
-    fixed activation of the right shape."""
+    back in one graph (the whole forward is one HIP graph replay; `reps` replays are timed). The attention cores
+    between in-proj and out-proj are out of scope: the out-proj reads a fixed activation of the right shape.
+    Returns the measurement as a dict."""
     M, H, I = 539, 5120, 17408
     dev = "cuda"
     g = torch.Generator(device=dev).manual_seed(5)
@@ -287,7 +293,7 @@ def main_stack(args, pkg, ext, perf):
             h, hn = ext.mm_residual_rmsnorm(h, m, d["w_dn"], w1, None, 1e-6)
         return h, hn
 
-    t = perf.gpu_time([forward], iters=1, reps=args.steps, warmup=2)
+    t = perf.gpu_time([forward], iters=1, reps=reps, warmup=2)
     flops = nbytes = 0.0
     for i in range(64):
         full = (i % 4) == 3
@@ -297,11 +303,17 @@ def main_stack(args, pkg, ext, perf):
             flops += f
             nbytes += b
     t_roof = max(nbytes / perf.HBM_PEAK, flops / perf.MFMA_BF16_PEAK)
-    print(json.dumps({"stack": "64-layer projection stack (48 lin + 16 full)", "M": M, "ms": round(t * 1e3, 3),
-                      "tflops": round(flops / t / 1e12, 1), "gbs": round(nbytes / t / 1e9, 1),
-                      "roof_ms": round(t_roof * 1e3, 3), "frac": round(t_roof / t, 4),
-                      "bound": "hbm" if nbytes / perf.HBM_PEAK >= flops / perf.MFMA_BF16_PEAK else "mfma"}),
-          flush=True)
+    del layers
+    torch.cuda.empty_cache()
+    return {"stack": "64-layer projection stack (48 lin + 16 full), one graph replay per forward", "M": M,
+            "weight_layout": "packed" if PACKED else "row-major", "ms": round(t * 1e3, 3),
+            "tflops": round(flops / t / 1e12, 1), "gbs": round(nbytes / t / 1e9, 1),
+            "roof_ms": round(t_roof * 1e3, 3), "frac": round(t_roof / t, 4),
+            "bound": "hbm" if nbytes / perf.HBM_PEAK >= flops / perf.MFMA_BF16_PEAK else "mfma"}
+
+
+def main_stack(args, pkg, ext, perf):
+    print(json.dumps(run_stack(ext, perf, args.steps)), flush=True)
 
 
 def main_head(args, pkg, ext, perf):
@@ -444,6 +456,7 @@ def main():
     ap.add_argument("--shapes", default="")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-shapes", action="store_true")
+    ap.add_argument("--no-stack", action="store_true", help="leave out the 64-layer stack (configs[4]) keys")
     ap.add_argument("--rowmajor", action="store_true", help="row-major weights instead of the packed layout")
     args = ap.parse_args()
     ws = int(os.environ.get("WORLD_SIZE", "1"))

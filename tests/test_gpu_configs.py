@@ -218,6 +218,91 @@ def test_stack_64_layers_graph(pkg, ext, O, dev):
     torch.cuda.empty_cache()
 
 
+def test_stack_64_layers_packed_fastproj(pkg, ext, O, dev):
+    """The same 64-layer stack (M = 539) the way a FastQwen35-shaped model runs it: weights
+    merged and packed at load by FastProjections.merge_linear_attn / merge_full_attn / merge_mlp (the layout
+    bench.py --stack times), and each layer driven through _mm, _res, _mm_silu and _res (src/fastmodel.py:412,
+    477-481). One HIP graph of the whole forward; three replays bit-equal to the eager run, with eager work in
+    between; the first and last layers against the oracle (row-major weights kept on the CPU for those two) on
+    sampled rows."""
+    fp, _ = _fastproj(pkg)
+    M, H, I = 539, 5120, 17408
+    lin_in, full_in, out_k = 16384, 14336, 6144
+    P = fp.FastProjections(eps=1e-6)
+    layers, keep = [], {}
+    for i in range(64):
+        g = torch.Generator(device=dev).manual_seed(2000 + i)
+        full = i % 4 == 3
+        n_in = full_in if full else lin_in
+        w_in, w_out = [(torch.randn(*s, generator=g, device=dev) * 0.02).bfloat16() for s in ((n_in, H), (H, out_k))]
+        gate, up, w_dn = [(torch.randn(*s, generator=g, device=dev) * 0.02).bfloat16() for s in ((I, H), (I, H), (H, I))]
+        d = P.merge_mlp(gate, up, w_dn)
+        if full:   # cat[q, k, v]: q + gate rows, then k, then v
+            P.merge_full_attn(d, w_in[:12288], w_in[12288:13312], w_in[13312:], w_out)
+        else:      # cat[qkv, z, b, a]
+            P.merge_linear_attn(d, w_in[:10240], w_in[10240:16288], w_in[16288:16336], w_in[16336:], w_out)
+        assert d.w_in.dim() == 4 and d.w_out.dim() == 4 and d.w_gu_packed.dim() == 4 and d.w_down.dim() == 4
+        if i in (0, 63):
+            keep[i] = {"w_in": w_in.cpu(), "w_out": w_out.cpu(), "w_gu": ext.pack_gate_up(gate, up).cpu(),
+                       "w_dn": w_dn.cpu()}
+        del w_in, w_out, gate, up, w_dn
+        layers.append(d)
+    g = torch.Generator(device=dev).manual_seed(6)
+    h0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    hn0 = torch.randn(M, H, generator=g, device=dev).bfloat16()
+    y_att = torch.randn(M, out_k, generator=g, device=dev).bfloat16()
+    w1 = (1.0 + 0.1 * torch.randn(H, generator=g, device=dev)).float()
+
+    def forward(trace=None):
+        h, hn = h0, hn0
+        for d in layers:
+            proj = P._mm(hn, d.w_in)
+            h1, hn1 = P._res(h, y_att, d.w_out_sk, d.sk_out, w1, None)
+            m = P._mm_silu(hn1, d.w_gu_packed)
+            if trace is not None:
+                trace.append((h, hn, proj, h1, hn1, m))
+            h, hn = P._res(h1, m, d.w_down_sk, d.sk_down, w1, None)
+        return h, hn
+
+    _say("case packed stack eager")
+    trace = []
+    eh, ehn = forward(trace)
+    eh, ehn = eh.clone(), ehn.clone()
+    torch.cuda.synchronize()
+    rows = sample_idx(M, 6, torch.Generator().manual_seed(4), extra=(538,)).to(dev)
+    for li in (0, 63):
+        h_in, hn_in = trace[li][0], trace[li][1]
+        _say(f"case packed stack layer {li} vs oracle")
+        want = _stack_layer_oracle(O, rows, h_in[rows].cpu(), hn_in[rows].cpu(), y_att[rows].cpu(), keep[li],
+                                   w1.cpu())
+        h_out, hn_out = (trace[li + 1][0], trace[li + 1][1]) if li < 63 else (eh, ehn)
+        got = (trace[li][2], trace[li][3], trace[li][4], trace[li][5], h_out, hn_out)
+        for name, a, b in zip(("proj", "h_att", "hn_att", "m", "h", "hn"), got, want):
+            _assert_tol(O, a[rows], b, f"layer {li} {name}")
+    del trace, keep
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        forward()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    _say("case packed stack capture")
+    with torch.cuda.graph(graph):
+        gh, ghn = forward()
+    for r in range(3):
+        _say(f"case packed stack replay {r}")
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(gh, eh) and torch.equal(ghn, ehn), f"replay {r} differs from the eager forward"
+        junk = P._mm_silu(hn0, layers[r].w_gu_packed)  # eager work between replays
+        torch.cuda.synchronize()
+        del junk
+    del graph, layers
+    torch.cuda.empty_cache()
+
+
 # --------------------------------------------------------------------------------------- drop-in shim
 def _fastproj(pkg):
     from importlib import import_module
