@@ -46,13 +46,20 @@ enum {
  * tail_rows rows of W (outputs N - tail_rows .. N - 1) run as a second launch with their own tile and split: when
  * N / BN tiles leave a few tiles over a whole number of rounds on the 256 CUs, a finer tile for the remainder
  * replaces a second, mostly idle round. tail_rows = 0 (the zero-initialised default) means no tail; tails apply
- * to ojx_gemm_bf16 and ojx_gemm_silu_mul (tail_rows a multiple of 8 there). */
+ * to ojx_gemm_bf16 and ojx_gemm_silu_mul (tail_rows a multiple of 8 there).
+ * one_launch = 1 (skinny tile family 0, splitk >= 2, no tail): the split-K reduction and its epilogue run in the
+ * GEMM launch itself (the last split of each tile to finish sums the fp32 planes), and for
+ * ojx_gemm_residual_rmsnorm the RMSNorm too (the last tile of each row block to finish normalises its rows): one
+ * launch instead of two. Results equal the two-launch path's bit for bit, except hn, whose sum of squares is added
+ * in another order (one rounding step at most). Its arrival counters are the library's (zero at load, left zero by
+ * every call): one-launch calls that overlap in time on one GPU race. */
 typedef struct {
   int32_t tile;
   int32_t splitk;
   int32_t tail_tile;
   int32_t tail_splitk;
   int32_t tail_rows;
+  int32_t one_launch;
 } ojx_cfg;
 
 const char* ojx_last_error(void);

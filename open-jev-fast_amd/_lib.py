@@ -19,11 +19,12 @@ _f32 = ctypes.c_float
 
 class OjxCfg(ctypes.Structure):
     _fields_ = [("tile", ctypes.c_int32), ("splitk", ctypes.c_int32), ("tail_tile", ctypes.c_int32),
-                ("tail_splitk", ctypes.c_int32), ("tail_rows", ctypes.c_int32)]
+                ("tail_splitk", ctypes.c_int32), ("tail_rows", ctypes.c_int32), ("one_launch", ctypes.c_int32)]
 
     def __repr__(self):
         t = f", tail {self.tail_rows} rows: tile {self.tail_tile} S {self.tail_splitk}" if self.tail_rows else ""
-        return f"OjxCfg(tile {self.tile}, S {self.splitk}{t})"
+        o = ", one launch" if self.one_launch else ""
+        return f"OjxCfg(tile {self.tile}, S {self.splitk}{t}{o})"
 
 
 _cfgp = ctypes.POINTER(OjxCfg)
@@ -105,8 +106,9 @@ def check(rc: int) -> None:
         raise RuntimeError(f"ojx error {rc}: {lib().ojx_last_error().decode()}")
 
 
-def cfg(tile: int, splitk: int, tail_tile: int = 0, tail_splitk: int = 1, tail_rows: int = 0) -> OjxCfg:
-    return OjxCfg(tile, splitk, tail_tile, tail_splitk, tail_rows)
+def cfg(tile: int, splitk: int, tail_tile: int = 0, tail_splitk: int = 1, tail_rows: int = 0,
+        one_launch: int = 0) -> OjxCfg:
+    return OjxCfg(tile, splitk, tail_tile, tail_splitk, tail_rows, one_launch)
 
 
 def plan(M: int, N: int, K: int, kind: int = KIND_PLAIN) -> OjxCfg:

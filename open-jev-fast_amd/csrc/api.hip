@@ -38,7 +38,7 @@ inline bool is_packed_kind(int32_t kind) { return (kind & OJX_KIND_PACKED) != 0;
 
 struct PlanEntry {
   int64_t M, N, K;
-  int32_t kind, tile, splitk, tail_tile, tail_splitk, tail_rows;
+  int32_t kind, tile, splitk, tail_tile, tail_splitk, tail_rows, one_launch;
 };
 
 // Measured on MI355X by the offline sweep (tuning script in the package); shapes not listed use heuristic_plan.
@@ -120,8 +120,17 @@ bool cfg_fits_packed(int64_t N, int64_t K, const ojx_cfg& c) {
   return (c.splitk - 1) * kchunk_pk(K, c.splitk) < K;
 }
 
+// One-launch split-K: family 0 with a real split and no tail, within the counters and 32-bit plane offsets.
+bool one_launch_fits(int64_t M, int64_t N, const ojx_cfg& c) {
+  if (c.one_launch == 0) return true;
+  const ojx::TileInfo* t = ojx::tile_info(c.tile);
+  if (c.one_launch != 1 || t == nullptr || t->family != 0 || c.splitk < 2 || c.tail_rows != 0) return false;
+  const int64_t tm = cdiv(M > 0 ? M : 1, t->bm), tn = cdiv(N, t->bn);
+  return tm * tn <= ojx::kOlMaxTiles && tm <= ojx::kOlMaxBlocks && (int64_t)c.splitk * M * N * 4 < (1LL << 31);
+}
+
 bool cfg_fits(int64_t M, int64_t N, int64_t K, const ojx_cfg& c, bool packed = false) {
-  (void)M;
+  if (!one_launch_fits(M, N, c)) return false;
   if (packed) return cfg_fits_packed(N, K, c);
   if (!part_fits(K, c.tile, c.splitk)) return false;
   if (c.tail_rows == 0) return true;
@@ -140,11 +149,15 @@ int64_t part_ws_bytes(const ojx_cfg& c, int64_t M, int64_t n, int64_t K) {
     const SkPlan sp = sk_plan(ojx::tile_info(c.tile), M, n, K, c.splitk);
     return sp.slot_bytes;
   }
+  if (c.one_launch) {  // the planes, then the per-tile row sums of squares
+    const ojx::TileInfo* t = ojx::tile_info(c.tile);
+    return cdiv((int64_t)c.splitk * M * n * 4, 256) * 256 + cdiv(cdiv(n, t->bn) * M * 4, 256) * 256;
+  }
   return c.splitk > 1 ? cdiv((int64_t)c.splitk * M * n * 4, 256) * 256 : 0;
 }
 int split_parts(const ojx_cfg& c, int64_t M, int64_t N, int64_t K, Part out[2]) {
   const int64_t nt = c.tail_rows;
-  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0}, 0, N - nt, 0};
+  out[0] = Part{ojx_cfg{c.tile, c.splitk, 0, 1, 0, c.one_launch}, 0, N - nt, 0};
   if (nt == 0) return 1;
   const int64_t ws0 = cdiv(part_ws_bytes(out[0].c, M, N - nt, K), 256) * 256;
   out[1] = Part{ojx_cfg{c.tail_tile, c.tail_splitk, 0, 1, 0}, N - nt, nt, ws0};
@@ -234,6 +247,20 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.sk_ws = nullptr;
   p.dp_tiles = 0;
   p.sk_grid = 0;
+  p.one_launch = 0;
+  p.ol_parts = nullptr;
+  p.ol_ss = nullptr;
+  p.w1 = w1;
+  p.rowmask = rowmask;
+  p.eps = eps;
+  p.hn = nullptr;
+  if (c.one_launch && c.splitk > 1) {
+    if (ws == nullptr) return fail(OJX_ERR_WORKSPACE, "one-launch split-K plan needs a workspace");
+    p.one_launch = 1;
+    p.ol_parts = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off);
+    p.ol_ss = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off + cdiv((int64_t)c.splitk * M * N * 4, 256) * 256);
+    p.hn = hn_out;
+  }
   int grid = 0;
   if (t->family == 5) {
     const SkPlan sp = sk_plan(t, M, N, K, c.splitk);
@@ -247,7 +274,7 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
     }
   }
   if ((int64_t)p.tiles_n * p.tiles_m * p.splits >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "grid too large");
-  if (hn_out != nullptr)
+  if (hn_out != nullptr && t->family == 5)
     return hip_check(ojx::launch_gemm_residual_rmsnorm_sk(c.tile, p, w1, rowmask, eps, hn_out, st, grid),
                      "gemm + row pass launch");
   return hip_check(ojx::launch_gemm(c.tile, epi, p, st, grid), "gemm launch");
@@ -355,7 +382,7 @@ int ojx_plan(int64_t M, int64_t N, int64_t K, int32_t kind, ojx_cfg* out) {
   const bool packed = is_packed_kind(kind);
   for (const PlanEntry& e : kPlan) {
     if (e.M == M && e.N == N && e.K == K && e.kind == kind) {
-      ojx_cfg c{e.tile, e.splitk, e.tail_tile, e.tail_splitk, e.tail_rows};
+      ojx_cfg c{e.tile, e.splitk, e.tail_tile, e.tail_splitk, e.tail_rows, e.one_launch};
       if (c.tail_splitk == 0) c.tail_splitk = 1;
       if (cfg_fits(M, N, K, c, packed)) { *out = c; return OJX_OK; }
     }
@@ -374,11 +401,13 @@ static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c, bool
   return true;
 }
 
+// Candidates: every (tile, split) that fits, and for the skinny family 0 with a split the one-launch variant too.
 int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind) {
   const bool packed = is_packed_kind(kind);
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
-    for (int s : kSplits) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}, packed) ? 1 : 0;
+    for (int s : kSplits)
+      for (int ol = 0; ol < 2; ++ol) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0, ol}, packed) ? 1 : 0;
   return n;
 }
 
@@ -388,10 +417,11 @@ int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, oj
   int n = 0;
   for (int t = 0; t < ojx::num_tiles(); ++t)
     for (int s : kSplits)
-      if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0}, packed)) {
-        if (n == idx) { *out = ojx_cfg{t, s, 0, 1, 0}; return OJX_OK; }
-        ++n;
-      }
+      for (int ol = 0; ol < 2; ++ol)
+        if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0, ol}, packed)) {
+          if (n == idx) { *out = ojx_cfg{t, s, 0, 1, 0, ol}; return OJX_OK; }
+          ++n;
+        }
   return fail(OJX_ERR_CONFIG, "candidate index %d out of range [0, %d)", idx, n);
 }
 
@@ -417,6 +447,7 @@ int ojx_gemm_splitk_f32(const void* x, const void* w, float* parts, int64_t M, i
   if (is_sk(c.tile))
     return fail(OJX_ERR_CONFIG, "tile %d (persistent stream-K family) has no split-K planes", c.tile);
   c.splitk = S;
+  c.one_launch = 0;  // planes out, no reduction
   if (!cfg_fits(M, N, K, c))
     return fail(OJX_ERR_CONFIG, "split-K S=%d (tile %d) invalid for K=%lld", S, c.tile, (long long)K);
   return gemm(c, ojx::EPI_F32, x, ldx, w, ldw, parts, N, nullptr, 0, M, N, K, static_cast<hipStream_t>(stream));
@@ -442,7 +473,7 @@ static int gemm_bf16_impl(const void* x, const void* w, void* y, int64_t M, int6
     const Part& q = parts[i];
     const void* wq = static_cast<const uint16_t*>(w) + q.n0 * ldw;
     uint16_t* yq = static_cast<uint16_t*>(y) + q.n0;
-    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
+    if (q.c.splitk == 1 || is_sk(q.c.tile) || q.c.one_launch) {
       OJX_TRY(gemm(q.c, ojx::EPI_BF16, x, ldx, wq, ldw, yq, ldy, nullptr, 0, M, q.n, K, st,
                    workspace, q.ws, nullptr, nullptr, 0.f, nullptr, packed));
       continue;
@@ -475,7 +506,7 @@ static int gemm_silu_mul_impl(const void* x, const void* w_gu_packed, void* out,
     const Part& q = parts[i];
     const void* wq = static_cast<const uint16_t*>(w_gu_packed) + q.n0 * K;
     uint16_t* oq = static_cast<uint16_t*>(out) + q.n0 / 2;  // packed blocks of 8 rows give 4 output columns
-    if (q.c.splitk == 1 || is_sk(q.c.tile)) {
+    if (q.c.splitk == 1 || is_sk(q.c.tile) || q.c.one_launch) {
       OJX_TRY(gemm(q.c, ojx::EPI_SILU, x, K, wq, K, oq, I, nullptr, 0, M, q.n, K, st,
                    workspace, q.ws, nullptr, nullptr, 0.f, nullptr, packed));
       continue;
@@ -512,6 +543,11 @@ static int gemm_residual_rmsnorm_impl(const void* x, const void* w, const void* 
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* h = static_cast<uint16_t*>(h_out);
   uint16_t* hn = static_cast<uint16_t*>(hn_out);
+  if (c.one_launch && c.splitk > 1) {  // GEMM, split reduction, residual and RMSNorm in one launch
+    OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
+    return gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, w1, rowmask, eps,
+                hn, packed);
+  }
   if (c.splitk == 1 || is_sk(c.tile)) {
     OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
     if (hn != nullptr && is_sk(c.tile) && sk_plan(ojx::tile_info(c.tile), M, N, K, c.splitk).partial) {

@@ -7,6 +7,7 @@ namespace ojx {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // Buffer loads: the descriptor's byte range makes out-of-range lanes read zeros without a branch, so predicated
 // tile loads stay in flight (a branch around each load would make the compiler drain the load queue at the join).
@@ -72,6 +73,29 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Cache policy of device-coherent accesses (sc0 sc1): stores written through to the level every XCD reads, loads
+// served from there. For data exchanged between workgroups of one launch, which may run on different XCDs whose L2s
+// are not coherent with each other.
+constexpr int kCoh = 1 | 16;
+
+// Sum over the S fp32 planes (plane stride ps elements) of the float4 at byte offset off, in ascending plane order,
+// with device-coherent loads; the loads go out eight planes at a time (indices clamped, extras not added).
+__device__ __forceinline__ f32x4 sum_planes_coh(__amdgpu_buffer_rsrc_t r, uint32_t off, int S, int64_t ps) {
+  f32x4 a = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoh));
+  for (int s0 = 1; s0 < S; s0 += 8) {
+    f32x4 c[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int64_t s = s0 + u < S ? s0 + u : S - 1;
+      c[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (uint32_t)(off + s * ps * 4), 0, kCoh));
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (s0 + u < S) a += c[u];
+  }
+  return a;
 }
 
 // 16-byte global -> LDS DMA: lane i of the wave writes lds + 16 i. (Kept out of the kernel templates: written

@@ -91,7 +91,17 @@ struct GemmParams {
   int wpk;                          // 1: W is in the stage-major packed layout (see ojx_pack_weight)
   FattnParams fa;                   // EPI_FATTN only
   int sk_grid;                      // workgroups that share the remaining tiles' K iterations
+  // one-launch split-K (family 0, splits > 1): the fp32 planes, the split reduction with its epilogue and, for the
+  // residual epilogue with hn, the rows' RMSNorm all run in the GEMM launch (see ol_epilogue in gemm.hip)
+  int one_launch;
+  float* ol_parts;                  // [S, M, N] fp32 planes (workspace)
+  float* ol_ss;                     // [tiles_n, M] fp32 sums of h^2 over each N tile's columns (workspace)
+  const float* w1; const int32_t* rowmask; float eps;
+  uint16_t* hn;                     // RMSNorm output [M, N] of the residual epilogue (null: h only)
 };
+
+// Arrival counters of the one-launch split-K (gemm.hip): per tile and per M block of a launch.
+constexpr int kOlMaxTiles = 16384, kOlMaxBlocks = 4096;
 
 struct TileInfo {
   int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M

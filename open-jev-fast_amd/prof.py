@@ -26,6 +26,7 @@ def main():
     ap.add_argument("--k", type=int, default=0)
     ap.add_argument("--tile", type=int, default=-1)
     ap.add_argument("--splitk", type=int, default=1)
+    ap.add_argument("--one-launch", type=int, default=0, help="with --tile: the one-launch split-K variant")
     ap.add_argument("--calls", type=int, default=40)
     ap.add_argument("--copy-mb", type=int, default=0)
     ap.add_argument("--packed", action="store_true", help="weights in the packed layout (ext.pack_weight)")
@@ -47,7 +48,7 @@ def main():
     N, K, kind = perf.SHAPES[args.shape]
     N, K = args.n or N, args.k or K
     M = args.m
-    cfg = pkg._lib.cfg(args.tile, args.splitk) if args.tile >= 0 else None
+    cfg = pkg._lib.cfg(args.tile, args.splitk, one_launch=args.one_launch) if args.tile >= 0 else None
     x = torch.randn(M, K, device="cuda").bfloat16()
     ws = [(torch.randn(N, K, device="cuda") * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
     if args.packed:

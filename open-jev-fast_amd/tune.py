@@ -102,7 +102,7 @@ def main():
                     wgs = -(-N // info["bn"]) * -(-M // info["bm"]) * c.splitk
                     if wgs > args.max_waves * 256:
                         continue
-                timed((c.tile, c.splitk, 0, 1, 0))
+                timed((c.tile, c.splitk, 0, 1, 0, c.one_launch))
             if kind != "residual" and not args.no_tails and not args.packed:
                 # tail configurations: the best simple tiles over whole rounds of 256 workgroups, the leftover
                 # rows with a finer tile
@@ -111,7 +111,7 @@ def main():
                 for t, key in simple:
                     if len(seen) == 4:
                         break
-                    if key[0] not in seen and _lib.tile_info(key[0])["family"] != 5:
+                    if key[0] not in seen and _lib.tile_info(key[0])["family"] != 5 and not key[5]:
                         seen.append(key[0])
                         mains += [(key[0], 1), (key[0], 2)]
                 tails = [c for c in _lib.candidates(M, N, K, kid) if c.splitk <= 4 and (only is None or c.tile in only)
@@ -129,7 +129,7 @@ def main():
                         ti = _lib.tile_info(c.tile)
                         if -(-tr // ti["bn"]) * -(-M // ti["bm"]) * c.splitk > 512:
                             continue
-                        timed((tile, S, c.tile, c.splitk, tr))
+                        timed((tile, S, c.tile, c.splitk, tr, 0))
             results.sort()
             # accept the fastest candidate whose numerics pass
             ref = None
@@ -156,7 +156,8 @@ def main():
                     best = (t, key)
                     break
                 print(json.dumps({"shape": name, "M": M, "cfg": key, "numerics": "FAIL"}), flush=True)
-            top = [{"us": round(t * 1e6, 2), "tile": k[0], "splitk": k[1], **({"tail": k[2:]} if k[4] else {})}
+            top = [{"us": round(t * 1e6, 2), "tile": k[0], "splitk": k[1], **({"tail": k[2:5]} if k[4] else {}),
+                    **({"one_launch": 1} if k[5] else {})}
                    for t, k in (results if args.all else results[:6])]
             if best is None:
                 print(json.dumps({"shape": name, "M": M, "error": "no valid candidate", "top": top}), flush=True)
@@ -164,7 +165,7 @@ def main():
             t, key = best
             r = perf.roofline(M, N, K, kind, t)
             print(json.dumps({"shape": name, "M": M, "N": N, "K": K, "kind": kind, "tile": key[0],
-                              "splitk": key[1], "tail": key[2:], "us": round(t * 1e6, 2),
+                              "splitk": key[1], "tail": key[2:5], "one_launch": key[5], "us": round(t * 1e6, 2),
                               "frac": round(r["frac"], 4), "tflops": round(r["tflops"], 1),
                               "gbs": round(r["gbs"], 1), "top": top}), flush=True)
             rows.append((M, N, K, kid, key, t))
@@ -172,7 +173,7 @@ def main():
         torch.cuda.empty_cache()
     if args.out:
         with open(args.out, "w") as f:
-            f.write("// {M, N, K, kind, tile, splitk, tail_tile, tail_splitk, tail_rows} measured by "
+            f.write("// {M, N, K, kind, tile, splitk, tail_tile, tail_splitk, tail_rows, one_launch} measured by "
                     "open-jev-fast_amd/tune.py on MI355X (us in comment)\n")
             for M, N, K, kid, key, t in rows:
                 f.write(f"{{{M}, {N}, {K}, {kid}, {', '.join(str(v) for v in key)}}},  // {t * 1e6:.1f} us\n")

@@ -60,6 +60,8 @@ def test_plan_valid_for_every_contract_shape(pkg, kind):
                 sk = True
             elif S > 1:
                 data += -(-S * M * n * 4 // 256) * 256
+                if c.one_launch:  # the per-tile row sums of squares follow the planes
+                    data += -(-(-(-n // pkg._lib.tile_info(tile)["bn"])) * M * 4 // 256) * 256
         if sk:
             assert ws >= data
         else:
@@ -69,7 +71,9 @@ def test_plan_valid_for_every_contract_shape(pkg, kind):
 def test_candidates(pkg):
     cands = pkg._lib.candidates(288, 5120, 5120)
     assert len(cands) > 10
-    assert len({(c.tile, c.splitk) for c in cands}) == len(cands)
+    assert len({(c.tile, c.splitk, c.one_launch) for c in cands}) == len(cands)
+    ol = [c for c in cands if c.one_launch]
+    assert ol and all(pkg._lib.tile_info(c.tile)["family"] == 0 and c.splitk >= 2 for c in ol)
     # no tile whose x rows are mostly padding at M = 7
     for c in pkg._lib.candidates(7, 5120, 5120):
         assert pkg._lib.tile_info(c.tile)["bm"] == 16
