@@ -631,7 +631,7 @@ static int check_fattn(int64_t N, int32_t HQ, int32_t HKV, int32_t D, int32_t RD
   if (HQ < 1 || HKV < 1 || HQ > 4096 || HKV > 4096) return fail(OJX_ERR_SHAPE, "bad head counts HQ=%d HKV=%d", HQ, HKV);
   if (RD < 16 || RD > D || RD % 16 != 0 || ((RD / 16) & (RD / 16 - 1)) != 0)
     return fail(OJX_ERR_SHAPE, "rotary dims RD=%d must be 16 * a power of two, <= D", RD);
-  if (N < 0 || N >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "bad token count");
+  if (N < 0 || N * ((HQ + 2 * HKV + 3) / 4) >= (1LL << 31)) return fail(OJX_ERR_SHAPE, "bad token count");
   if (N == 0) return OJX_OK;  // nothing is read or written
   const void* ptrs[] = {qw1, kw1, cosb, sinb, qt, kt, vt, gate};
   for (const void* q : ptrs)

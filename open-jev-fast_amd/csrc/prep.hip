@@ -34,89 +34,79 @@ __device__ __forceinline__ void unpack4(uint2 a, float (&v)[4]) {
 //   d < RD/2 and xn[d - RD/2] for RD/2 <= d < RD; dims >= RD keep xn.
 //   Outputs: qt [HQ, N, D], kt [HKV, N, D], vt [HKV, N, D] (head-major for attention) and gate [N, HQ D].
 //
-// Work layout: one workgroup of four waves per token. The gate and v parts are pure copies, done first by all 256
-// lanes as 16-byte moves. The HQ + HKV normalised heads are then taken in rounds of four, one head per wave, with
-// lane l owning dims 4l .. 4l+3 (one 8-byte load, one 8-byte store, 512 contiguous bytes per wave). The head's
-// sum of squares is a 64-lane wave total. The normalised head goes to the wave's 1 KB LDS row, from which each
-// lane of the rotary part reads the four partner values xn[d -+ RD/2] after a workgroup barrier.
+// Work layout: one wave per (token, head task), four tasks per workgroup. Task t of a token: t < HQ the q head t
+// (the wave also copies gate head t), HQ <= t < HQ + HKV the k head t - HQ, then the v heads (copies). Lane l owns
+// dims 4l .. 4l+3 (one 8-byte load, one 8-byte store: 512 contiguous bytes per wave). A q/k head's sum of squares
+// is a 64-lane wave total; the normalised head goes to the wave's own 1 KB of LDS, from which each lane of the
+// rotary part reads its four partner values xn[d -+ RD/2] (a wave-local exchange: no workgroup barrier).
 __global__ void __launch_bounds__(256) fullattn_prep_k(const uint16_t* __restrict__ proj, int64_t N, int HQ, int HKV,
                                                        int RD, float eps, const float* __restrict__ qw1,
                                                        const float* __restrict__ kw1, const uint16_t* __restrict__ cosb,
                                                        const uint16_t* __restrict__ sinb, uint16_t* __restrict__ qt,
                                                        uint16_t* __restrict__ kt, uint16_t* __restrict__ vt,
                                                        uint16_t* __restrict__ gate) {
-  constexpr int D = 256, CH = D / 8;  // 16-byte chunks per head
+  constexpr int D = 256;
   __shared__ float4 xn_lds[4][D / 4];
-  const int64_t n = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int T = HQ + 2 * HKV, G = (T + 3) >> 2;  // tasks per token, workgroups per token
+  const int64_t n = blockIdx.x / G;
+  const int t = (int)(blockIdx.x - n * G) * 4 + wave;
+  if (t >= T) return;  // whole wave; no workgroup barrier follows
   const int64_t P = (int64_t)(2 * HQ + 2 * HKV) * D;
   const uint16_t* row = proj + n * P;
-
-  // copies: gate heads (HQ x CH chunks), then v heads (HKV x CH chunks)
-  for (int i = tid; i < (HQ + HKV) * CH; i += 256) {
-    const int h = i / CH, c = (i - h * CH) * 8;
-    if (h < HQ) {
-      *reinterpret_cast<uint4*>(gate + n * (int64_t)(HQ * D) + h * D + c) =
-          *reinterpret_cast<const uint4*>(row + (int64_t)h * 2 * D + D + c);
-    } else {
-      const int hv = h - HQ;
-      *reinterpret_cast<uint4*>(vt + ((int64_t)hv * N + n) * D + c) =
-          *reinterpret_cast<const uint4*>(row + (int64_t)(2 * HQ + HKV) * D + hv * D + c);
-    }
-  }
-
   const int d0 = lane * 4;
-  const bool rot = d0 < RD;
-  float cs[4] = {1.f, 1.f, 1.f, 1.f}, sn[4] = {0.f, 0.f, 0.f, 0.f};
-  if (rot) {
-    unpack4(*reinterpret_cast<const uint2*>(cosb + n * RD + d0), cs);
-    unpack4(*reinterpret_cast<const uint2*>(sinb + n * RD + d0), sn);
+  if (t >= HQ + HKV) {  // v head: a copy into [HKV, N, D]
+    const int hv = t - HQ - HKV;
+    *reinterpret_cast<uint2*>(vt + ((int64_t)hv * N + n) * D + d0) =
+        *reinterpret_cast<const uint2*>(row + (int64_t)(2 * HQ + HKV) * D + hv * D + d0);
+    return;
   }
-  const int pd = d0 < RD / 2 ? d0 + RD / 2 : d0 - RD / 2;  // partner dims (used on the rotary part only)
-  const float sgn = d0 < RD / 2 ? -1.f : 1.f;
-  const int T = HQ + HKV;
-  for (int base = 0; base < T; base += 4) {  // uniform trip count: every wave meets every barrier
-    const int t = base + wave;
-    const bool live = t < T;
-    const bool isq = t < HQ;
-    float xn[4] = {0.f, 0.f, 0.f, 0.f};
-    if (live) {
-      const uint16_t* src = row + (isq ? (int64_t)t * 2 * D : (int64_t)2 * HQ * D + (int64_t)(t - HQ) * D) + d0;
-      float x[4];
-      unpack4(*reinterpret_cast<const uint2*>(src), x);
-      float ss = x[0] * x[0];
-      ss += x[1] * x[1];
-      ss += x[2] * x[2];
-      ss += x[3] * x[3];
-      const float r = rsqrtf(wave_total(ss) / (float)D + eps);
-      const float4 w = *reinterpret_cast<const float4*>((isq ? qw1 : kw1) + d0);
-      xn[0] = rbf((x[0] * r) * w.x);
-      xn[1] = rbf((x[1] * r) * w.y);
-      xn[2] = rbf((x[2] * r) * w.z);
-      xn[3] = rbf((x[3] * r) * w.w);
-      xn_lds[wave][lane] = make_float4(xn[0], xn[1], xn[2], xn[3]);
-    }
-    __syncthreads();
-    if (live) {
-      float o[4] = {xn[0], xn[1], xn[2], xn[3]};
-      if (rot) {
-        const float4 p = xn_lds[wave][pd >> 2];
-        const float pv[4] = {p.x, p.y, p.z, p.w};
+  const bool isq = t < HQ;
+  if (isq)  // gate head: a copy into [N, HQ D]
+    *reinterpret_cast<uint2*>(gate + n * (int64_t)(HQ * D) + t * D + d0) =
+        *reinterpret_cast<const uint2*>(row + (int64_t)t * 2 * D + D + d0);
+  float x[4];
+  unpack4(*reinterpret_cast<const uint2*>(row + (isq ? (int64_t)t * 2 * D : (int64_t)2 * HQ * D + (int64_t)(t - HQ) * D)
+                                          + d0), x);
+  float ss = x[0] * x[0];
+  ss += x[1] * x[1];
+  ss += x[2] * x[2];
+  ss += x[3] * x[3];
+  const float r = rsqrtf(wave_total(ss) / (float)D + eps);
+  const float4 w = *reinterpret_cast<const float4*>((isq ? qw1 : kw1) + d0);
+  float xn[4];
+  xn[0] = rbf((x[0] * r) * w.x);
+  xn[1] = rbf((x[1] * r) * w.y);
+  xn[2] = rbf((x[2] * r) * w.z);
+  xn[3] = rbf((x[3] * r) * w.w);
+  float o[4] = {xn[0], xn[1], xn[2], xn[3]};
+  if (RD > 0) {
+    xn_lds[wave][lane] = make_float4(xn[0], xn[1], xn[2], xn[3]);
+    // the wave's LDS writes are complete and visible to its own lanes before the partner reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    if (d0 < RD) {
+      float cs[4], sn[4];
+      unpack4(*reinterpret_cast<const uint2*>(cosb + n * RD + d0), cs);
+      unpack4(*reinterpret_cast<const uint2*>(sinb + n * RD + d0), sn);
+      const bool lo = d0 < RD / 2;
+      const float4 pq = xn_lds[wave][(lo ? d0 + RD / 2 : d0 - RD / 2) >> 2];
+      const float pv[4] = {pq.x, pq.y, pq.z, pq.w};
 #pragma unroll
-        for (int j = 0; j < 4; ++j) o[j] = rbf(rbf(xn[j] * cs[j]) + rbf((sgn * pv[j]) * sn[j]));
-      }
-      uint16_t* dst = isq ? qt + ((int64_t)t * N + n) * D : kt + ((int64_t)(t - HQ) * N + n) * D;
-      *reinterpret_cast<uint2*>(dst + d0) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
+      for (int j = 0; j < 4; ++j) o[j] = rbf(rbf(xn[j] * cs[j]) + rbf((lo ? -pv[j] : pv[j]) * sn[j]));
     }
-    __syncthreads();  // the LDS row is rewritten by the next round
   }
+  uint16_t* dst = isq ? qt + ((int64_t)t * N + n) * D : kt + ((int64_t)(t - HQ) * N + n) * D;
+  *reinterpret_cast<uint2*>(dst + d0) = make_uint2(pack2(o[0], o[1]), pack2(o[2], o[3]));
 }
 
 hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV, int RD, float eps,
                                 const float* qw1, const float* kw1, const uint16_t* cosb, const uint16_t* sinb,
                                 uint16_t* qt, uint16_t* kt, uint16_t* vt, uint16_t* gate, hipStream_t st) {
-  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)N), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps, qw1, kw1, cosb,
-                     sinb, qt, kt, vt, gate);
+  const int64_t G = (HQ + 2 * HKV + 3) / 4;
+  hipLaunchKernelGGL(fullattn_prep_k, dim3((unsigned)(N * G)), dim3(256), 0, st, proj, N, HQ, HKV, RD, eps, qw1, kw1,
+                     cosb, sinb, qt, kt, vt, gate);
   return hipGetLastError();
 }
 
@@ -137,20 +127,22 @@ hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV
 // Products of two bf16 values are exact in fp32, so the conv's sum order is the only one that fixes its bits; it is
 // kept. The head sums of squares are added in another order than the reference's (one rounding step at most).
 //
-// Work layout: one workgroup of four waves per packed row, grid = N rows + the padding groups.
+// Work layout: one workgroup of 16 waves (1024 lanes) per packed row, grid = N rows + the padding groups.
 //   1. conv + SiLU for all C channels (8 per lane per step, the four history rows and the 64 weight bytes as 16-byte
-//      loads), the bf16 results kept in an LDS copy of the row;
+//      loads; 10240 channels take 1.25 steps), the bf16 results kept in an LDS copy of the row;
 //   2. one q/k head per wave at a time, 2 channels per lane: wave-total sum of squares, scaled in place in LDS;
 //      lanes below HV compute the gates into LDS meanwhile;
 //   3. the finished row is written slot after slot: every 16-byte chunk of a slot's q | k | v row is one lane's
 //      LDS read and global store, so each slot row goes out as one contiguous sweep; slot ids come in through
-//      LDS, 256 at a time.
+//      LDS, 1024 at a time.
 // A padding group (the workgroups after the N row workgroups) writes zero rows to kPadSlots consecutive
 // padding slots.
-constexpr int kPadSlots = 32;
+constexpr int kPadSlots = 8;
+
+constexpr int kLinThreads = 512;
 
 template <int RQ>
-__global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict__ proj, const int4* __restrict__ hist,
+__global__ void __launch_bounds__(kLinThreads) linattn_prep_k(const uint16_t* __restrict__ proj, const int4* __restrict__ hist,
                                                      const int* __restrict__ rep_ptr, const int* __restrict__ rep_pos,
                                                      const uint16_t* __restrict__ convw,
                                                      const uint16_t* __restrict__ A_log,
@@ -165,6 +157,7 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int n = blockIdx.x;
   const bool pad = n >= N;
+  const int4 hr = hist[min(n, N)];  // row N holds no history; issued beside the rep_ptr loads
   int p0, p1;
   if (!pad) {
     p0 = rep_ptr[n];
@@ -178,12 +171,14 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
   uint16_t* orow = reinterpret_cast<uint16_t*>(lds_raw);                 // [C] bf16 bits
   float* gl = reinterpret_cast<float*>(orow + C);                         // [HV] g
   uint16_t* bl = reinterpret_cast<uint16_t*>(gl + HV);                    // [HV] beta bits
-  int* slot = reinterpret_cast<int*>(lds_raw) + (C * 2 + HV * 6 + 15) / 16 * 4;  // [256] slot ids
+  int* slot = reinterpret_cast<int*>(lds_raw) + (C * 2 + HV * 6 + 15) / 16 * 4;  // [kLinThreads] slot ids
+  // the first batch of slot ids is fetched now, so that its latency overlaps the row's compute
+  const int cnt0 = min(kLinThreads, p1 - p0);
+  const int sid0 = tid < cnt0 ? rep_pos[p0 + tid] : 0;
 
   if (!pad) {
-    const int4 hr = hist[n];
     const int rows[4] = {hr.x, hr.y, hr.z, hr.w};
-    for (int c0 = tid * 8; c0 < C; c0 += 256 * 8) {
+    for (int c0 = tid * 8; c0 < C; c0 += kLinThreads * 8) {
       uint4 xr[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -222,7 +217,7 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
     }
     __syncthreads();
     // q / k heads: one per wave at a time, channels 2 lane, 2 lane + 1
-    for (int h = wave; h < 2 * KD / HD; h += 4) {
+    for (int h = wave; h < 2 * KD / HD; h += kLinThreads / 64) {
       uint32_t* pr = reinterpret_cast<uint32_t*>(orow + h * HD) + lane;
       const uint32_t u = *pr;
       const float a = bf2f(u & 0xffffu), b = bf2f(u >> 16);
@@ -236,13 +231,13 @@ __global__ void __launch_bounds__(256) linattn_prep_k(const uint16_t* __restrict
 
   // scatter: chunk u of a slot row is q (u < QC), k (QC <= u < 2 QC) or v; q/k rows hold each head RQ times
   const int QC = RQ * KD / 8, VC = VD / 8, U = 2 * QC + VC;
-  for (int base = p0; base < p1; base += 256) {
-    const int cnt = min(256, p1 - base);
-    if (tid < cnt) slot[tid] = rep_pos[base + tid];
+  for (int base = p0; base < p1; base += kLinThreads) {
+    const int cnt = min(kLinThreads, p1 - base);
+    if (tid < cnt) slot[tid] = base == p0 ? sid0 : rep_pos[base + tid];
     __syncthreads();
     for (int j = 0; j < cnt; ++j) {
       const int64_t s = slot[j];
-      for (int u = tid; u < U; u += 256) {
+      for (int u = tid; u < U; u += kLinThreads) {
         uint4 val = make_uint4(0u, 0u, 0u, 0u);
         uint16_t* dst;
         int src;
@@ -274,13 +269,13 @@ hipError_t launch_linattn_prep(const uint16_t* proj, const int32_t* hist, const 
                                const uint16_t* A_log, const uint16_t* dt_bias, int KD, int VD, int HV, int RQ,
                                uint16_t* q, uint16_t* k, uint16_t* v, float* g, uint16_t* beta, hipStream_t st) {
   const int C = 2 * KD + VD;
-  const size_t lds = (size_t)((C * 2 + HV * 6 + 15) / 16) * 16 + 256 * sizeof(int);
+  const size_t lds = (size_t)((C * 2 + HV * 6 + 15) / 16) * 16 + kLinThreads * sizeof(int);
   const dim3 grid((unsigned)(N + (R + kPadSlots - 1) / kPadSlots));
   if (RQ == 3)
-    hipLaunchKernelGGL(linattn_prep_k<3>, grid, dim3(256), lds, st, proj, reinterpret_cast<const int4*>(hist),
+    hipLaunchKernelGGL(linattn_prep_k<3>, grid, dim3(kLinThreads), lds, st, proj, reinterpret_cast<const int4*>(hist),
                        rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
   else
-    hipLaunchKernelGGL(linattn_prep_k<1>, grid, dim3(256), lds, st, proj, reinterpret_cast<const int4*>(hist),
+    hipLaunchKernelGGL(linattn_prep_k<1>, grid, dim3(kLinThreads), lds, st, proj, reinterpret_cast<const int4*>(hist),
                        rep_ptr, rep_pos, convw, A_log, dt_bias, q, k, v, g, beta, (int)N, KD, VD, HV);
   return hipGetLastError();
 }
