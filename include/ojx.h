@@ -47,12 +47,14 @@ enum {
  * N / BN tiles leave a few tiles over a whole number of rounds on the 256 CUs, a finer tile for the remainder
  * replaces a second, mostly idle round. tail_rows = 0 (the zero-initialised default) means no tail; tails apply
  * to ojx_gemm_bf16 and ojx_gemm_silu_mul (tail_rows a multiple of 8 there).
- * one_launch = 1 (skinny tile family 0, splitk >= 2, no tail): the split-K reduction and its epilogue run in the
- * GEMM launch itself (the last split of each tile to finish sums the fp32 planes), and for
- * ojx_gemm_residual_rmsnorm the RMSNorm too (the last tile of each row block to finish normalises its rows): one
- * launch instead of two. Results equal the two-launch path's bit for bit, except hn, whose sum of squares is added
- * in another order (one rounding step at most). Its arrival counters are the library's (zero at load, left zero by
- * every call): one-launch calls that overlap in time on one GPU race. */
+ * one_launch = 1 (tile families 0 and 6, splitk >= 2, no tail): the split-K reduction and its epilogue run in the
+ * GEMM launch itself (the last split of each tile to finish sums the fp32 planes, in split order); for
+ * ojx_gemm_residual_rmsnorm the launch ends with h and a second launch normalises h (instead of reading the
+ * planes). one_launch = 2 (family 0, ojx_gemm_residual_rmsnorm): the RMSNorm too (the last tile of each row block
+ * to finish normalises its rows): one launch instead of two. Results equal the two-launch path's bit for bit,
+ * except hn under one_launch = 2, whose sum of squares is added in another order (one rounding step at most). The
+ * arrival counters are the library's (zero at load, left zero by every call): one-launch calls that overlap in
+ * time on one GPU race. */
 typedef struct {
   int32_t tile;
   int32_t splitk;

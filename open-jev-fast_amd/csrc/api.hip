@@ -124,7 +124,10 @@ bool cfg_fits_packed(int64_t N, int64_t K, const ojx_cfg& c) {
 bool one_launch_fits(int64_t M, int64_t N, const ojx_cfg& c) {
   if (c.one_launch == 0) return true;
   const ojx::TileInfo* t = ojx::tile_info(c.tile);
-  if (c.one_launch != 1 || t == nullptr || t->family != 0 || c.splitk < 2 || c.tail_rows != 0) return false;
+  if (t == nullptr || c.splitk < 2 || c.tail_rows != 0) return false;
+  // 1: the skinny family 0 or the K-interleaved family 6; 2 (the RMSNorm fold too): family 0 only
+  if (!(c.one_launch == 1 && (t->family == 0 || t->family == 6)) && !(c.one_launch == 2 && t->family == 0))
+    return false;
   const int64_t tm = cdiv(M > 0 ? M : 1, t->bm), tn = cdiv(N, t->bn);
   return tm * tn <= ojx::kOlMaxTiles && tm <= ojx::kOlMaxBlocks && (int64_t)c.splitk * M * N * 4 < (1LL << 31);
 }
@@ -254,12 +257,15 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.rowmask = rowmask;
   p.eps = eps;
   p.hn = nullptr;
+  p.ol_tiles = p.ol_blocks = nullptr;
   if (c.one_launch && c.splitk > 1) {
     if (ws == nullptr) return fail(OJX_ERR_WORKSPACE, "one-launch split-K plan needs a workspace");
-    p.one_launch = 1;
+    const int rc = hip_check(ojx::ol_counters(&p.ol_tiles, &p.ol_blocks), "one-launch counters");
+    if (rc != OJX_OK) return rc;
+    p.one_launch = c.one_launch;
     p.ol_parts = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off);
     p.ol_ss = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off + cdiv((int64_t)c.splitk * M * N * 4, 256) * 256);
-    p.hn = hn_out;
+    p.hn = c.one_launch == 2 ? hn_out : nullptr;
   }
   int grid = 0;
   if (t->family == 5) {
@@ -405,9 +411,10 @@ static bool candidate_ok(int64_t M, int64_t N, int64_t K, const ojx_cfg& c, bool
 int ojx_num_candidates(int64_t M, int64_t N, int64_t K, int32_t kind) {
   const bool packed = is_packed_kind(kind);
   int n = 0;
+  const int nol = (kind & ~OJX_KIND_PACKED) == OJX_KIND_RESIDUAL ? 3 : 2;  // the RMSNorm fold: residual only
   for (int t = 0; t < ojx::num_tiles(); ++t)
     for (int s : kSplits)
-      for (int ol = 0; ol < 2; ++ol) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0, ol}, packed) ? 1 : 0;
+      for (int ol = 0; ol < nol; ++ol) n += candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0, ol}, packed) ? 1 : 0;
   return n;
 }
 
@@ -415,9 +422,10 @@ int ojx_candidate(int64_t M, int64_t N, int64_t K, int32_t kind, int32_t idx, oj
   const bool packed = is_packed_kind(kind);
   if (out == nullptr) return fail(OJX_ERR_ARG, "null candidate output");
   int n = 0;
+  const int nol = (kind & ~OJX_KIND_PACKED) == OJX_KIND_RESIDUAL ? 3 : 2;
   for (int t = 0; t < ojx::num_tiles(); ++t)
     for (int s : kSplits)
-      for (int ol = 0; ol < 2; ++ol)
+      for (int ol = 0; ol < nol; ++ol)
         if (candidate_ok(M, N, K, ojx_cfg{t, s, 0, 1, 0, ol}, packed)) {
           if (n == idx) { *out = ojx_cfg{t, s, 0, 1, 0, ol}; return OJX_OK; }
           ++n;
@@ -543,10 +551,15 @@ static int gemm_residual_rmsnorm_impl(const void* x, const void* w, const void* 
   hipStream_t st = static_cast<hipStream_t>(stream);
   uint16_t* h = static_cast<uint16_t*>(h_out);
   uint16_t* hn = static_cast<uint16_t*>(hn_out);
-  if (c.one_launch && c.splitk > 1) {  // GEMM, split reduction, residual and RMSNorm in one launch
+  if (c.one_launch && c.splitk > 1) {
+    // one_launch 2: GEMM, split reduction, residual and RMSNorm in one launch; 1: the GEMM launch ends with h, and
+    // the RMSNorm is a second launch over h (instead of over the S fp32 planes)
     OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));
-    return gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, w1, rowmask, eps,
-                hn, packed);
+    OJX_TRY(gemm(c, ojx::EPI_RESID, x, K, w, K, h_out, N, residual, N, M, N, K, st, workspace, 0, w1, rowmask, eps,
+                 hn, packed));
+    if (hn == nullptr || c.one_launch == 2) return OJX_OK;
+    return hip_check(ojx::launch_add_rmsnorm(h, nullptr, nullptr, 0, 0, w1, rowmask, eps, nullptr, hn, (int)M,
+                                             (int)N, st), "rmsnorm launch");
   }
   if (c.splitk == 1 || is_sk(c.tile)) {
     OJX_TRY(check_ws(workspace, workspace_bytes, workspace_for(c, M, N, K)));

@@ -25,142 +25,31 @@
 namespace ojx {
 
 // ------------------------------------------------------------------------------------------------ one launch
-// Arrival counters of the one-launch split-K: zero when the library loads, and every call leaves the counters it
-// used at zero again (the last arrival re-arms its counter). Calls of one-launch plans that run at the same time
-// on one GPU (different streams) share them and race.
+// Arrival counters of the one-launch split-K (ol_epilogue, gemm_common.h): zero when the library loads, and every
+// call leaves the counters it used at zero again (the last arrival re-arms its counter). Calls of one-launch plans
+// that run at the same time on one GPU (different streams) share them and race.
 __device__ uint32_t g_ol_tiles[kOlMaxTiles];
 __device__ uint32_t g_ol_blocks[kOlMaxBlocks];
 
-// Counts the calling workgroup in *ctr (agent scope) after all its threads' device-coherent stores have completed,
-// and returns on every thread whether it was the last of `expect` arrivals; the last re-arms the counter. No
-// workgroup waits for another: the last one does the follow-up work, so the launch cannot deadlock whatever order
-// or residency its workgroups get.
-__device__ __forceinline__ bool ol_arrive(uint32_t* ctr, uint32_t expect) {
-  __shared__ uint32_t last;
-  wait_vmcnt<0>();  // this thread's stores are at the coherent level
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t old = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    last = old + 1 == expect ? 1u : 0u;
-    if (last) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Device addresses of the counters on the current device (looked up once per device, with it current).
+hipError_t ol_counters(uint32_t** tiles, uint32_t** blocks) {
+  static uint32_t* cache[64][2];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+  if (cache[dev][0] == nullptr) {
+    void* t = nullptr;
+    void* b = nullptr;
+    if ((e = hipGetSymbolAddress(&t, HIP_SYMBOL(g_ol_tiles))) != hipSuccess) return e;
+    if ((e = hipGetSymbolAddress(&b, HIP_SYMBOL(g_ol_blocks))) != hipSuccess) return e;
+    if (t == nullptr || b == nullptr) return hipErrorInvalidSymbol;
+    cache[dev][1] = static_cast<uint32_t*>(b);
+    cache[dev][0] = static_cast<uint32_t*>(t);
   }
-  __syncthreads();
-  return last != 0u;
-}
-
-// After each split of tile (tn, tm) has stored its fp32 plane (device-coherent stores): the last split to arrive
-// sums the tile's S planes in split order, the arithmetic and order of reduce_bf16_k / reduce_silu_k /
-// add_rmsnorm_k (epilogue.hip), and stores the epilogue's result. With the residual epilogue and hn it also stores
-// the tile's per-row sums of h^2 (over its BN columns, in column order), and the last tile of the M block to
-// arrive normalises the block's rows: r = rsqrt(sum over the N tiles, in tile order, / N + eps), hn = bf16((h r) w1),
-// zero on masked rows. The bits of y, out and h equal the two-launch path's; hn's sum of squares is added in
-// another order than add_rmsnorm_k's (a rounding step at most). `lds` is the kernel's operand LDS, free by now.
-template <int BN, int BM, int NT>
-__device__ void ol_epilogue(const GemmParams& p, const int epi, const int tn, const int tm, float* lds) {
-  const int M = p.M, N = p.N, S = p.splits;
-  if (!ol_arrive(&g_ol_tiles[tn * p.tiles_m + tm], (uint32_t)S)) return;
-  const int n0 = tn * BN, m0 = tm * BM, tid = threadIdx.x;
-  const int64_t ps = (int64_t)M * N;
-  const __amdgpu_buffer_rsrc_t rsP = make_rsrc(p.ol_parts, S * ps * 4);
-  const bool norm = epi == EPI_RESID && p.hn != nullptr;
-  // h of the residual epilogue, read back by the row pass (possibly on another XCD): one descriptor over [M, ldo]
-  const __amdgpu_buffer_rsrc_t rsH = make_rsrc(p.out, (int64_t)M * p.ldo * 2);
-  // groups of 4 columns (8 for the SiLU.mul pairs: 4 gate then 4 up columns give 4 outputs)
-  const int gw = epi == EPI_SILU ? 8 : 4, gpr = BN / gw;
-  for (int it = tid; it < BM * gpr; it += NT) {
-    const int mi = it / gpr, n = n0 + (it - mi * gpr) * gw, m = m0 + mi;
-    float hsq = 0.f;
-    if (m < M && n < N) {
-      const uint32_t off = (uint32_t)(((int64_t)m * N + n) * 4);
-      if (epi == EPI_SILU) {
-        f32x4 g = sum_planes_coh(rsP, off, S, ps), u = sum_planes_coh(rsP, off + 16, S, ps);
-        uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
-        uint32_t o[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(g[e]))) * rbf(u[e]));
-        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
-      } else {
-        const f32x4 a = sum_planes_coh(rsP, off, S, ps);
-        uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
-        if (epi == EPI_RESID) {
-          const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
-          const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
-          float h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = rbf(rv[e] + rbf(a[e]));
-          hsq = h[0] * h[0];
-          hsq += h[1] * h[1];
-          hsq += h[2] * h[2];
-          hsq += h[3] * h[3];
-          const uint2 hv = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-          if (norm)
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, hv), rsH, (uint32_t)(((int64_t)m * p.ldo + n) * 2), 0, kCoh);
-          else
-            *reinterpret_cast<uint2*>(dst) = hv;
-        } else {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3]));
-        }
-      }
-    }
-    if (norm) lds[it] = hsq;
-  }
-  if (!norm) return;
-  // the tile's row sums of h^2, in column order
-  __syncthreads();
-  const __amdgpu_buffer_rsrc_t rsS = make_rsrc(p.ol_ss, (int64_t)p.tiles_n * M * 4);
-  if (tid < BM && m0 + tid < M) {
-    float s = 0.f;
-    for (int c = 0; c < gpr; ++c) s += lds[tid * gpr + c];
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s), rsS, (uint32_t)(((int64_t)tn * M + m0 + tid) * 4), 0, kCoh);
-  }
-  if (!ol_arrive(&g_ol_blocks[tm], (uint32_t)p.tiles_n)) return;
-  // the block's row pass over all N columns
-  float* rr = lds;  // [BM] 1 / rms
-  if (tid < BM && m0 + tid < M) {
-    float s = 0.f;
-    for (int t0 = 0; t0 < p.tiles_n; t0 += 16) {  // 16 loads in flight, added in tile order
-      float v[16];
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsS, (uint32_t)(((int64_t)min(t0 + u, p.tiles_n - 1) * M + m0 + tid) * 4),
-                                             0, kCoh));
-#pragma unroll
-      for (int u = 0; u < 16; ++u)
-        if (t0 + u < p.tiles_n) s += v[u];
-    }
-    rr[tid] = rsqrtf(s / (float)N + p.eps);
-  }
-  __syncthreads();
-  // 8 items (8 columns each) per thread per batch: the h loads of a batch go out together
-  const int cpr = N >> 3, items = (min(M, m0 + BM) - m0) * cpr;
-  constexpr int U = 8;
-  for (int i0 = 0; i0 < items; i0 += NT * U) {
-    uint4 hv[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int it = i0 + u * NT + tid, mi = it / cpr, n = (it - mi * cpr) * 8;
-      hv[u] = it < items ? __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(
-                               rsH, (uint32_t)(((int64_t)(m0 + mi) * p.ldo + n) * 2), 0, kCoh))
-                         : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int it = i0 + u * NT + tid;
-      if (it >= items) continue;
-      const int mi = it / cpr, n = (it - mi * cpr) * 8, m = m0 + mi;
-      const float4 wa = *reinterpret_cast<const float4*>(p.w1 + n), wb = *reinterpret_cast<const float4*>(p.w1 + n + 4);
-      const float wv[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
-      const uint32_t hw[4] = {hv[u].x, hv[u].y, hv[u].z, hv[u].w};
-      const bool keep = p.rowmask == nullptr || p.rowmask[m] != 0;
-      const float r = rr[mi];
-      float o[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = keep ? (bf2f((hw[j >> 1] >> ((j & 1) * 16)) & 0xffffu) * r) * wv[j] : 0.f;
-      *reinterpret_cast<uint4*>(p.hn + (int64_t)m * N + n) =
-          make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
-    }
-  }
+  *tiles = cache[dev][0];
+  *blocks = cache[dev][1];
+  return hipSuccess;
 }
 
 template <int BN, int BM, int BK, int WN, int WM>

@@ -391,6 +391,25 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
     return;
   }
   // lane holds v[e] = y[m][n + e]: m = m0 + 16 xf + lr, n = n0 + 16 wf + 4 lg
+  if constexpr (EPI != EPI_F32) {
+    if (p.one_launch) {  // this split's fp32 plane, then the tile's last split reduces (gemm_common.h)
+      const __amdgpu_buffer_rsrc_t rsP = make_rsrc(p.ol_parts, (int64_t)p.splits * p.M * p.N * 4);
+      const int64_t zo = (int64_t)z * p.M * p.N;
+#pragma unroll
+      for (int f = 0; f < NACC; ++f) {
+        if ((f < HF) != (h == 0)) continue;
+        const int wf = f < FW * FX ? wfrag(f / FX) : wfrag(f - FW * FX);
+        const int xf = f < FW * FX ? g * FX + f % FX : xe;
+        if (f >= FW * FX && wf < wnom) continue;  // stored by the neighbouring group
+        const int m = m0 + xf * 16 + lr, n = n0 + wf * 16 + lg * 4;
+        const f32x4 v = f < FW * FX ? acc[f / FX][f % FX] : acce[f - FW * FX];
+        if (m < p.M && n < p.N)
+          __builtin_amdgcn_raw_buffer_store_b128(v, rsP, (uint32_t)((zo + (int64_t)m * p.N + n) * 4), 0, kCoh);
+      }
+      ol_epilogue<BN, BM, 512>(p, EPI, tn, tm, reinterpret_cast<float*>(smem));
+      return;
+    }
+  }
 #pragma unroll
   for (int f = 0; f < NACC; ++f) {
     if ((f < HF) != (h == 0)) continue;

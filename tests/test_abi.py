@@ -73,7 +73,10 @@ def test_candidates(pkg):
     assert len(cands) > 10
     assert len({(c.tile, c.splitk, c.one_launch) for c in cands}) == len(cands)
     ol = [c for c in cands if c.one_launch]
-    assert ol and all(pkg._lib.tile_info(c.tile)["family"] == 0 and c.splitk >= 2 for c in ol)
+    assert ol and all(pkg._lib.tile_info(c.tile)["family"] in (0, 6) and c.splitk >= 2 for c in ol)
+    assert all(c.one_launch == 1 for c in ol)  # the RMSNorm fold (2) is a residual candidate only
+    fold = [c for c in pkg._lib.candidates(7, 5120, 6144, 2) if c.one_launch == 2]
+    assert fold and all(pkg._lib.tile_info(c.tile)["family"] == 0 for c in fold)
     # no tile whose x rows are mostly padding at M = 7
     for c in pkg._lib.candidates(7, 5120, 5120):
         assert pkg._lib.tile_info(c.tile)["bm"] == 16

@@ -1,11 +1,12 @@
-"""GPU parity of the one-launch split-K plans (ojx_cfg.one_launch = 1, skinny tile family 0), through the C-ABI.
+"""GPU parity of the one-launch split-K plans (ojx_cfg.one_launch, tile families 0 and 6), through the C-ABI.
 
-The last split of each tile to finish sums the fp32 planes in split order and applies the epilogue inside the GEMM
-launch; for the residual kind with hn, the last tile of each row block to finish normalises the block's rows
-(the reference's separate add_rmsnorm_sk2 launch, src/kernels.cu:1444-1501, src/fastmodel.py:196-203). Checked:
-* y (plain), out (SiLU.mul) and h (residual) equal the two-launch path with the same tile and split bit for bit
-  (the same sums in the same order); hn within one bf16 rounding step (its sum of squares is added in another
-  order) and mostly equal; masked rows zero;
+one_launch = 1: the last split of each tile to finish sums the fp32 planes in split order and applies the epilogue
+inside the GEMM launch (the residual kind ends with h; a second launch normalises h). one_launch = 2 (family 0,
+residual): the last tile of each row block to finish also normalises the block's rows (the reference's separate
+add_rmsnorm_sk2 launch, src/kernels.cu:1444-1501, src/fastmodel.py:196-203). Checked:
+* y (plain), out (SiLU.mul), h and hn (residual, one_launch = 1) equal the two-launch path with the same tile and
+  split bit for bit (the same sums in the same order); under one_launch = 2, hn within one bf16 rounding step (its
+  sum of squares is added in another order) and mostly equal; masked rows zero;
 * row-major and packed weights, ragged M / N / K, splits 2 .. 16;
 * back-to-back calls and HIP graph replays (the arrival counters re-arm themselves);
 * the north star's tolerance against the oracle at full size (o_proj, down, QKV, gate-up at M = 1 / 7 / 16).
@@ -22,9 +23,9 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _skinny_tiles(pkg):
+def _one_launch_tiles(pkg):
     L = pkg._lib
-    return [t for t in range(L.lib().ojx_num_tiles()) if L.tile_info(t)["family"] == 0]
+    return [t for t in range(L.lib().ojx_num_tiles()) if L.tile_info(t)["family"] in (0, 6)]
 
 
 def _close_hn(got, want, what):
@@ -56,8 +57,9 @@ def test_one_launch_equals_two_launches(pkg, ext, dev, M, N, K, packed):
     mmr = ext.mm_residual_rmsnorm_pk if packed else ext.mm_residual_rmsnorm
     mms = ext.mm_silu_mul_pk if packed else ext.mm_silu_mul
     W = wu if packed else w
-    for t in _skinny_tiles(pkg):
-        for S in (2, 3, 8, 16):
+    for t in _one_launch_tiles(pkg):
+        fam = pkg._lib.tile_info(t)["family"]
+        for S in ((2, 3, 8, 16) if fam == 0 else (2, 3)):
             two, one = (t, S, 0, 1, 0, 0), (t, S, 0, 1, 0, 1)
             _say(f"case one-launch M={M} N={N} K={K} packed={packed} tile={t} S={S}")
             try:
@@ -73,12 +75,20 @@ def test_one_launch_equals_two_launches(pkg, ext, dev, M, N, K, packed):
                 h2, hn2 = mmr(res, x, W, w1, m, 1e-6, cfg=two)
                 h1, hn1 = mmr(res, x, W, w1, m, 1e-6, cfg=one)
                 torch.cuda.synchronize()
-                assert torch.equal(h1, h2), f"h tile {t} S {S}"
-                _close_hn(hn1, hn2, f"hn tile {t} S {S} mask {m is not None}")
-                if m is not None:
-                    assert bool((hn1[m == 0] == 0).all())
+                assert torch.equal(h1, h2) and torch.equal(hn1, hn2), f"residual tile {t} S {S}"
                 h3 = mmr(res, x, W, w1, None, 1e-6, want_hn=False, cfg=one)[0]
-                assert torch.equal(h3, h2)
+                assert torch.equal(h3, h2 if m is None else mmr(res, x, W, w1, None, 1e-6, cfg=two)[0])
+                if fam != 0:
+                    continue
+                fold = (t, S, 0, 1, 0, 2)
+                hf, hnf = mmr(res, x, W, w1, m, 1e-6, cfg=fold)
+                assert torch.equal(hf, h2), f"fold h tile {t} S {S}"
+                _close_hn(hnf, hn2, f"fold hn tile {t} S {S} mask {m is not None}")
+                if m is not None:
+                    assert bool((hnf[m == 0] == 0).all())
+        if fam == 6:  # the fold is family 0's only
+            with pytest.raises(RuntimeError, match="invalid"):
+                mmr(res, x, W, w1, None, 1e-6, cfg=(t, 2, 0, 1, 0, 2))
 
 
 def test_one_launch_repeats_and_graph(pkg, ext, dev):
@@ -86,7 +96,7 @@ def test_one_launch_repeats_and_graph(pkg, ext, dev):
     call's bits."""
     x, w, res, w1, _ = _inputs(7, 5120, 6144, 11, dev)
     x2, w2, res2, w12, _ = _inputs(3, 1040, 1024, 12, dev)
-    one = (0, 8, 0, 1, 0, 1)
+    one = (0, 8, 0, 1, 0, 2)
     h0, hn0 = ext.mm_residual_rmsnorm(res, x, w, w1, None, 1e-6, cfg=one)
     y0 = ext.mm(x2, w2, cfg=(0, 4, 0, 1, 0, 1))
     h0, hn0, y0 = h0.clone(), hn0.clone(), y0.clone()
@@ -124,7 +134,7 @@ def test_one_launch_full_size_vs_oracle(pkg, ext, O, dev, shape, M):
     x, w, res, w1, _ = _inputs(M, N, K, 3 * M + N, dev)
     wp = ext.pack_weight(w)
     S = 8
-    one = (0, S, 0, 1, 0, 1)
+    one = (0, S, 0, 1, 0, 2 if kind == "residual" else 1)
     xc, wc = x.cpu(), w.cpu()
     if kind == "plain":
         got = ext.mm_pk(x, wp, cfg=one)
