@@ -134,6 +134,12 @@ int ojx_gemm_residual_rmsnorm(const void* x, const void* w, const void* residual
  * copy in a layout the kernels stream; the row-major W is no longer needed once packed. */
 int ojx_pack_weight(const void* w, void* wp, int64_t N, int64_t K, ojx_stream_t stream);
 
+/* The reference's split-K weight copy back to W: wsk [S, K/S, N] bf16 (wsk[s][k][n] = W[n][s K/S + k], made by _split,
+ * src/fastmodel.py:186-188, and taken by lt2_run, src/lt.cpp:58-59,160-169) -> w [N, K] row-major. For callers that
+ * hold only the reference's copy: the projections read W [N, K] (or its packed layout) and split K in place. N and
+ * K multiples of 8, K % S == 0. */
+int ojx_unsplit_weight(const void* wsk, void* w, int64_t N, int64_t K, int64_t S, ojx_stream_t stream);
+
 /* ojx_gemm_bf16 / ojx_gemm_silu_mul / ojx_gemm_residual_rmsnorm on a packed weight: same arguments and results (x
  * row-major as before), the weight in the ojx_pack_weight layout. Tile families 0, 5 and 6 read it; cfg NULL = the
  * plan for kind | OJX_KIND_PACKED; an explicit cfg must name a tile of those families, with no tail, and split-K

@@ -48,6 +48,7 @@ EXPORTS = {
     "ojx_gemm_residual_rmsnorm_noalloc": (ctypes.c_int, [_p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _i64, _cfgp,
                                                          _p]),
     "ojx_pack_weight": (ctypes.c_int, [_p, _p, _i64, _i64, _p]),
+    "ojx_unsplit_weight": (ctypes.c_int, [_p, _p, _i64, _i64, _i64, _p]),
     "ojx_gemm_bf16_pk": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _cfgp, _p]),
     "ojx_gemm_silu_mul_pk": (ctypes.c_int, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _cfgp, _p]),
     "ojx_gemm_residual_rmsnorm_pk": (ctypes.c_int, [_p, _p, _p, _p, _p, _f32, _p, _p, _i64, _i64, _i64, _p, _i64,

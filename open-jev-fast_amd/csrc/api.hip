@@ -616,6 +616,16 @@ int ojx_pack_weight(const void* w, void* wp, int64_t N, int64_t K, ojx_stream_t 
                                            static_cast<hipStream_t>(stream)), "pack launch");
 }
 
+int ojx_unsplit_weight(const void* wsk, void* w, int64_t N, int64_t K, int64_t S, ojx_stream_t stream) {
+  OJX_TRY(check_dims(1, N, K));
+  if (S < 1 || K % S != 0) return fail(OJX_ERR_SHAPE, "K=%lld is not a multiple of S=%lld", (long long)K, (long long)S);
+  if (wsk == nullptr || w == nullptr || !aligned(wsk, 16) || !aligned(w, 16))
+    return fail(OJX_ERR_ARG, "wsk and w must be non-null and 16-byte aligned");
+  if (K > 65535 * 64LL) return fail(OJX_ERR_SHAPE, "K=%lld too large (at most %lld)", (long long)K, 65535 * 64LL);
+  return hip_check(ojx::launch_unsplit_weight(static_cast<const uint16_t*>(wsk), static_cast<uint16_t*>(w), K, N,
+                                              static_cast<hipStream_t>(stream)), "unsplit launch");
+}
+
 int ojx_gemm_bf16_pk(const void* x, const void* wp, void* y, int64_t M, int64_t N, int64_t K, int64_t ldx,
                      int64_t ldy, void* workspace, int64_t workspace_bytes, const ojx_cfg* cfg, ojx_stream_t stream) {
   OJX_TRY(check_packed_shape(N, K));

@@ -178,6 +178,40 @@ __global__ void __launch_bounds__(256) pack_weight_k(const uint16_t* __restrict_
   *reinterpret_cast<uint4*>(wp + dst) = *reinterpret_cast<const uint4*>(w + n * K + k);
 }
 
+// The reference's split-K weight copy wsk [S, K/S, N] (src/fastmodel.py:186-188: wsk[s][k][n] = W[n][s K/S + k]) is
+// W^T [K, N] row-major once its first two dims are merged; back to W [N, K]: a transpose through LDS. One workgroup
+// per 64 x 64 block: 256 threads read 64 rows of 64 n (16 B each, two passes), then each writes 8 consecutive k of
+// one n (16 B), so both global sides are 128-byte row pieces. The LDS row pitch of 72 elements puts the 8 rows a
+// thread gathers on different banks. K and N are multiples of 8 (whole 16-byte pieces; partial blocks are guarded).
+__global__ void __launch_bounds__(256) unsplit_weight_k(const uint16_t* __restrict__ wt, uint16_t* __restrict__ w,
+                                                        int64_t K, int64_t N) {
+  __shared__ uint16_t t[64][72];
+  const int tid = threadIdx.x;
+  const int64_t k0 = (int64_t)blockIdx.y * 64, n0 = (int64_t)blockIdx.x * 64;
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int r = pass * 32 + (tid >> 3), c = (tid & 7) * 8;  // row k0 + r, columns n0 + c .. + 7
+    uint4 v = make_uint4(0u, 0u, 0u, 0u);
+    if (k0 + r < K && n0 + c < N) v = *reinterpret_cast<const uint4*>(wt + (k0 + r) * N + n0 + c);
+    const uint32_t e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      t[r][c + 2 * j] = (uint16_t)(e[j] & 0xffffu);
+      t[r][c + 2 * j + 1] = (uint16_t)(e[j] >> 16);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int pass = 0; pass < 2; ++pass) {
+    const int nr = pass * 32 + (tid >> 3), kc = (tid & 7) * 8;  // output row n0 + nr, k0 + kc .. + 7
+    if (n0 + nr >= N || k0 + kc >= K) continue;
+    uint32_t o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = (uint32_t)t[kc + 2 * j][nr] | ((uint32_t)t[kc + 2 * j + 1][nr] << 16);
+    *reinterpret_cast<uint4*>(w + (n0 + nr) * K + k0 + kc) = make_uint4(o[0], o[1], o[2], o[3]);
+  }
+}
+
 static inline unsigned nblocks(int64_t n, int t) { return (unsigned)((n + t - 1) / t); }
 
 // Scoring head (src/server.py:37,57,129: mdl.head(hn[lastidx].float()).squeeze(-1), a Linear(H, 1) on fp32):
@@ -266,6 +300,12 @@ hipError_t launch_pack_gate_up(const uint16_t* gate, const uint16_t* up, uint16_
                                hipStream_t st) {
   const int64_t n = (int64_t)2 * I * (K / 8);
   hipLaunchKernelGGL(pack_gate_up_k, dim3(nblocks(n, 256)), dim3(256), 0, st, gate, up, packed, I, K);
+  return hipGetLastError();
+}
+
+hipError_t launch_unsplit_weight(const uint16_t* wt, uint16_t* w, int64_t K, int64_t N, hipStream_t st) {
+  hipLaunchKernelGGL(unsplit_weight_k, dim3((unsigned)((N + 63) / 64), (unsigned)((K + 63) / 64)), dim3(256), 0, st,
+                     wt, w, K, N);
   return hipGetLastError();
 }
 

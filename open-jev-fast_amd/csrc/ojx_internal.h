@@ -152,5 +152,6 @@ hipError_t launch_linattn_prep(const uint16_t* proj, const int32_t* hist, const 
 // W [N, K] row-major -> packed [K/64][N/16][16][64]: the 16-row x 64-k blocks of one 64-k stage of all rows are
 // contiguous, so a tile's weights for one stage are one contiguous run (N % 16 == 0, K % 64 == 0).
 hipError_t launch_pack_weight(const uint16_t* w, uint16_t* wp, int64_t N, int64_t K, hipStream_t st);
+hipError_t launch_unsplit_weight(const uint16_t* wt, uint16_t* w, int64_t K, int64_t N, hipStream_t st);
 
 }  // namespace ojx

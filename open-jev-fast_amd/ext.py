@@ -19,6 +19,7 @@ the current stream's device and every launch goes on torch's current stream, so 
 CUDA/HIP graph.
 """
 import ctypes
+import weakref
 
 import torch
 
@@ -282,6 +283,37 @@ def pack_weight(w):
     wp = torch.empty((K // 64, N // 16, 16, 64), dtype=w.dtype, device=w.device)
     check(lib().ojx_pack_weight(_ptr(w), _ptr(wp), N, K, _stream()))
     return wp
+
+
+_UNSPLIT = {}   # id(split weight) -> (weak reference to it, its version, its address, W [N, K])
+
+
+def _unsplit_drop(key):
+    def drop(ref):  # the split weight died: forget its W, unless the id already names a newer tensor's entry
+        if _UNSPLIT.get(key, (None,))[0] is ref:
+            del _UNSPLIT[key]
+    return drop
+
+
+def unsplit_weight(wsk):
+    """W [N, K] from the reference's split-K copy wsk [S, K/S, N] (src/fastmodel.py:186-188; ojx_unsplit_weight), for
+    callers that hold only that copy (lt2_run / _skmm / _res with a weight from the reference's own _split). The
+    result is kept while wsk lives and is made again if wsk is modified in place; during a graph capture it is made
+    inside the capture and not kept (the graph's memory pool owns it)."""
+    _chk(wsk, "wsk", torch.bfloat16)
+    if wsk.dim() != 3:
+        raise RuntimeError(f"unsplit_weight: wsk must be [S, K/S, N], got {tuple(wsk.shape)}")
+    S, KS, N = wsk.shape
+    capturing = torch.cuda.is_current_stream_capturing()
+    key = id(wsk)
+    hit = None if capturing else _UNSPLIT.get(key)
+    if hit is not None and hit[0]() is wsk and hit[1] == wsk._version and hit[2] == wsk.data_ptr():
+        return hit[3]
+    w = torch.empty((N, S * KS), dtype=wsk.dtype, device=wsk.device)
+    check(lib().ojx_unsplit_weight(_ptr(wsk), _ptr(w), N, S * KS, S, _stream()))
+    if not capturing:
+        _UNSPLIT[key] = (weakref.ref(wsk, _unsplit_drop(key)), wsk._version, wsk.data_ptr(), w)
+    return w
 
 
 def _pk_shape(wp):

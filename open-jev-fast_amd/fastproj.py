@@ -43,10 +43,13 @@ def _nk(w):
 
 
 def _wsk_2d(wsk, what):
+    """W [N, K] (or packed) for a split-K weight: FastProjections._split returns W itself; the reference's own copy
+    [S, K/S, N] (src/fastmodel.py:186-188) is turned back into W once per tensor (ext.unsplit_weight)."""
+    if wsk.dim() == 3:
+        return ext.unsplit_weight(wsk)
     if wsk.dim() not in (2, 4):
-        raise RuntimeError(f"{what}: the split-K weight must be W itself, [N, K] or packed (FastProjections._split "
-                           f"returns it unchanged); got shape {tuple(wsk.shape)}, the reference's [S, K/S, N] copy "
-                           "(src/fastmodel.py:186-188), which libojx does not read")
+        raise RuntimeError(f"{what}: the split-K weight must be [N, K], packed [K/64, N/16, 16, 64] or the "
+                           f"reference's [S, K/S, N]; got shape {tuple(wsk.shape)}")
     return wsk
 
 
@@ -115,9 +118,10 @@ class FastProjections:
         """Tile for the split-K partial GEMM (_skmm): the residual plan's tile when it writes split-K planes, else -1
         (the library then picks a plane-writing tile itself; the persistent family has no K planes)."""
         M, K = y.shape
-        if _wsk_2d(wsk, "_tune_sk").dim() == 4:
+        W = _wsk_2d(wsk, "_tune_sk")
+        if W.dim() == 4:
             raise RuntimeError("_skmm / _tune_sk: the split-K plane GEMM takes a row-major W [N, K]")
-        N = wsk.shape[0]
+        N = W.shape[0]
         c = _lib.plan(M, N, K, _lib.KIND_RESIDUAL)
         tile = c.tile if _lib.tile_info(c.tile)["family"] != 5 else -1
         self._sk_best[(M, N, K, S)] = tile
@@ -134,11 +138,12 @@ class FastProjections:
     def _skmm(self, y, wsk, S):
         """parts [S, M, N] fp32 = the S K-chunks of y times W (the reference's torch.bmm / lt2_run)."""
         M, K = y.shape
-        key = (M, _wsk_2d(wsk, "_skmm").shape[0], K, S)
+        W = _wsk_2d(wsk, "_skmm")
+        key = (M, W.shape[0], K, S)
         tile = self._sk_best.get(key)
         if tile is None:
-            tile = self._tune_sk(y, wsk, S)
-        return ext.mm_splitk_f32(y, wsk, S, tile=tile)
+            tile = self._tune_sk(y, W, S)
+        return ext.mm_splitk_f32(y, W, S, tile=tile)
 
     def _silu_mul(self, gu):
         if LUT:

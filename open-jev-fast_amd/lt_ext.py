@@ -9,10 +9,10 @@
     LT.lt2_info(h, idx); LT.lt2_raw(h, idx); LT.lt2_add_raw(h, raw)                 (src/lt.cpp:170-190)
 
 A "candidate" is a (tile, split-K) pair of libojx rather than a cuBLASLt algorithm; a raw descriptor is that pair.
-Differences, on purpose: split-K weights stay [N, K]. A plan made with wl=1 (the reference's split-K layout
-[S, K/S, N], src/lt.cpp:58-59) still takes the [N, K] weight in lt2_run, because the kernel reads the K chunks of W
-in place; a 3-D [S, K/S, N] weight raises a RuntimeError that names the layout. Only fp32 partials exist (f32=0
-raises), which is what the reference uses.
+Differences, on purpose: the kernels read the K chunks of W [N, K] in place, so lt2_run takes W itself; the
+reference's split-K copy [S, K/S, N] (wl=1, src/lt.cpp:58-59) is also accepted and turned back into W once per
+weight tensor (ext.unsplit_weight, kept while that tensor lives). Only fp32 partials exist (f32=0 raises), which is
+what the reference uses.
 """
 import torch
 
@@ -72,12 +72,13 @@ class _LT:
         if not 0 <= idx < len(p["found"]):
             raise RuntimeError(f"candidate index {idx} out of range [0, {len(p['found'])})")
         M, N, K = p["shape"]
-        if w.dim() == 3:
-            raise RuntimeError(f"lt2_run: w has the reference's split-K layout [S, K/S, N] {tuple(w.shape)} "
-                               "(src/lt.cpp:58-59, wl=1); libojx reads the split-K chunks of W [N, K] in place, so "
-                               "pass W itself (FastProjections._split returns it)")
+        if w.dim() == 3:   # the reference's split-K copy [S, K/S, N] (src/lt.cpp:58-59, wl=1)
+            if tuple(w.shape) != (p["S"], K // p["S"], N) or K % p["S"]:
+                raise RuntimeError(f"w {tuple(w.shape)} does not match the plan's [S, K/S, N] = "
+                                   f"[{p['S']}, {K // p['S']}, {N}]")
+            w = ext.unsplit_weight(w)
         if tuple(x.shape) != (M, K) or tuple(w.shape) != (N, K):
-            raise RuntimeError("x / w do not match the plan's shape (w must be [N, K])")
+            raise RuntimeError("x / w do not match the plan's shape (w must be [N, K] or [S, K/S, N])")
         return ext.mm_splitk_f32(x, w, p["S"], tile=p["found"][idx])
 
     def lt2_info(self, h, idx):

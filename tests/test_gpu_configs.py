@@ -371,9 +371,12 @@ def test_fastprojections_reference_call_pattern(pkg, ext, O, dev, monkeypatch):
     _assert_tol(O, c(h3), rh2, "_res down h (split 2)")
     _assert_tol(O, c(hn3), rhn2, "_res down hn (split 2)")
 
-    ref_layout = w_down.view(H, 2, I // 2).permute(1, 2, 0).contiguous()  # the reference's _split result
-    with pytest.raises(RuntimeError, match=r"\[S, K/S, N\]"):
-        P._res(h1, m, ref_layout, 2, w1, mask)
+    # the reference's own _split result [S, K/S, N] (src/fastmodel.py:186-188) is read back as W
+    ref_layout = w_down.view(H, 2, I // 2).permute(1, 2, 0).contiguous()
+    h4, hn4 = P._res(h1, m, ref_layout, 2, w1, mask)
+    h5, hn5 = P._res(h1, m, w_down, 2, w1, mask)
+    assert torch.equal(h4, h5) and torch.equal(hn4, hn5), "_res on the reference's split layout"
+    _assert_tol(O, c(h4), rh2, "_res down h (reference split layout)")
 
 
 @pytest.mark.parametrize("M", [7, 288, 539])
@@ -405,8 +408,10 @@ def test_fastprojections_skmm_and_lt(pkg, ext, O, dev, M):
         p2 = LT.lt2_run(hdl, y, w, i)
         for s in range(2):
             _assert_tol(O, p2[s][rows], ref[s], f"lt2_run cand {i} part {s}")
-    with pytest.raises(RuntimeError, match=r"\[S, K/S, N\]"):
-        LT.lt2_run(hdl, y, w.view(H, 2, I // 2).permute(1, 2, 0).contiguous(), 0)
+    p3 = LT.lt2_run(hdl, y, w.view(H, 2, I // 2).permute(1, 2, 0).contiguous(), 0)  # the reference's layout
+    assert torch.equal(p3, LT.lt2_run(hdl, y, w, 0))
+    parts3 = P._skmm(y, w.view(H, 2, I // 2).permute(1, 2, 0).contiguous(), 2)
+    assert torch.equal(parts3, parts)
 
     _say(f"case lt_matmul M={M}")
     x = y[:, :H].contiguous()

@@ -216,6 +216,23 @@ def test_splitk_parts_match_reference_chunks(pkg, ext, O, dev):
     assert (parts - ref).abs().max().item() <= 1e-4 * ref.abs().max().item() + 1e-5
 
 
+@pytest.mark.parametrize("N,K,S", [(200, 216, 3), (72, 64, 8), (5120, 17408, 2)])
+def test_unsplit_weight_layout(pkg, ext, dev, N, K, S):
+    """The reference's split-K copy wsk [S, K/S, N] (src/fastmodel.py:186-188) back to W [N, K]: every element,
+    ragged blocks included; the result is kept per source tensor and remade after an in-place change."""
+    _say(f"case unsplit N={N} K={K} S={S}")
+    w = torch.randn(N, K, generator=torch.Generator().manual_seed(N + K), dtype=torch.float32).bfloat16().to(dev)
+    wsk = w.view(N, S, K // S).permute(1, 2, 0).contiguous()
+    u = ext.unsplit_weight(wsk)
+    assert u.shape == (N, K) and torch.equal(u, w)
+    assert ext.unsplit_weight(wsk) is u
+    wsk.mul_(2)
+    u2 = ext.unsplit_weight(wsk)
+    assert u2 is not u and torch.equal(u2, w * 2)
+    with pytest.raises(RuntimeError, match="multiples of 8"):
+        ext.unsplit_weight(torch.zeros(2, 8, 12, dtype=torch.bfloat16, device=dev))
+
+
 # ----------------------------------------------------------------------------------------------- epilogues
 def test_add_rmsnorm_variants(pkg, ext, O, dev):
     M, H = 33, 5120
