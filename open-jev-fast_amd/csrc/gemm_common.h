@@ -152,7 +152,7 @@ __device__ __forceinline__ bool ol_arrive(uint32_t* ctr, uint32_t expect) {
 // arrive normalises the block's rows: r = rsqrt(sum over the N tiles, in tile order, / N + eps), hn = bf16((h r) w1),
 // zero on masked rows. The bits of y, out and h equal the two-launch path's; hn's sum of squares is added in
 // another order than add_rmsnorm_k's (a rounding step at most). `lds` is the kernel's operand LDS, free by now.
-template <int BN, int BM, int NT>
+template <int BN, int BM, int NT, int URMAX = 1>
 __device__ __forceinline__ void ol_epilogue(const GemmParams& p, const int epi, const int tn, const int tm, float* lds) {
   const int M = p.M, N = p.N, S = p.splits;
   if (!ol_arrive(p.ol_tiles + tn * p.tiles_m + tm, (uint32_t)S)) return;
@@ -163,43 +163,96 @@ __device__ __forceinline__ void ol_epilogue(const GemmParams& p, const int epi, 
   // h of the residual epilogue, read back by the row pass (possibly on another XCD): one descriptor over [M, ldo]
   const __amdgpu_buffer_rsrc_t rsH = make_rsrc(p.out, (int64_t)M * p.ldo * 2);
   // groups of 4 columns (8 for the SiLU.mul pairs: 4 gate then 4 up columns give 4 outputs)
-  const int gw = epi == EPI_SILU ? 8 : 4, gpr = BN / gw;
-  for (int it = tid; it < BM * gpr; it += NT) {
-    const int mi = it / gpr, n = n0 + (it - mi * gpr) * gw, m = m0 + mi;
+  const int gw = epi == EPI_SILU ? 8 : 4, gpr = BN / gw, nitem = BM * gpr;
+  // the epilogue of one item from its plane sums (a; u: the up columns of a SiLU.mul pair); returns its sum of h^2
+  auto finish = [&](const int m, const int n, const f32x4 a, const f32x4 u) -> float {
     float hsq = 0.f;
-    if (m < M && n < N) {
-      const uint32_t off = (uint32_t)(((int64_t)m * N + n) * 4);
-      if (epi == EPI_SILU) {
-        f32x4 g = sum_planes_coh(rsP, off, S, ps), u = sum_planes_coh(rsP, off + 16, S, ps);
-        uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
-        uint32_t o[4];
+    if (epi == EPI_SILU) {
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + (n >> 1);
+      uint32_t o[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(g[e]))) * rbf(u[e]));
-        *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+      for (int e = 0; e < 4; ++e) o[e] = f2bf(rbf(silu_f(rbf(a[e]))) * rbf(u[e]));
+      *reinterpret_cast<uint2*>(dst) = make_uint2(o[0] | (o[1] << 16), o[2] | (o[3] << 16));
+    } else {
+      uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
+      if (epi == EPI_RESID) {
+        const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
+        const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
+        float h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = rbf(rv[e] + rbf(a[e]));
+        hsq = h[0] * h[0];
+        hsq += h[1] * h[1];
+        hsq += h[2] * h[2];
+        hsq += h[3] * h[3];
+        const uint2 hv = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        if (norm)
+          __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, hv), rsH,
+                                                (uint32_t)(((int64_t)m * p.ldo + n) * 2), 0, kCoh);
+        else
+          *reinterpret_cast<uint2*>(dst) = hv;
       } else {
-        const f32x4 a = sum_planes_coh(rsP, off, S, ps);
-        uint16_t* dst = reinterpret_cast<uint16_t*>(p.out) + (int64_t)m * p.ldo + n;
-        if (epi == EPI_RESID) {
-          const uint2 rr = *reinterpret_cast<const uint2*>(p.res + (int64_t)m * p.ldr + n);
-          const float rv[4] = {bf2f(rr.x & 0xffffu), bf2f(rr.x >> 16), bf2f(rr.y & 0xffffu), bf2f(rr.y >> 16)};
-          float h[4];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) h[e] = rbf(rv[e] + rbf(a[e]));
-          hsq = h[0] * h[0];
-          hsq += h[1] * h[1];
-          hsq += h[2] * h[2];
-          hsq += h[3] * h[3];
-          const uint2 hv = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
-          if (norm)
-            __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, hv), rsH, (uint32_t)(((int64_t)m * p.ldo + n) * 2), 0, kCoh);
-          else
-            *reinterpret_cast<uint2*>(dst) = hv;
-        } else {
-          *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3]));
-        }
+        *reinterpret_cast<uint2*>(dst) = make_uint2(pack2(a[0], a[1]), pack2(a[2], a[3]));
       }
     }
-    if (norm) lds[it] = hsq;
+    return hsq;
+  };
+  constexpr int UR0 = (BM * BN / 4 + NT - 1) / NT;
+  constexpr int UR = UR0 < URMAX ? UR0 : URMAX;
+  if constexpr (UR == 1) {
+    // one item at a time, its planes loaded 8 at a time
+    for (int it = tid; it < nitem; it += NT) {
+      const int mi = it / gpr, n = n0 + (it - mi * gpr) * gw, m = m0 + mi;
+      float hsq = 0.f;
+      if (m < M && n < N) {
+        const uint32_t off = (uint32_t)(((int64_t)m * N + n) * 4);
+        const f32x4 a = sum_planes_coh(rsP, off, S, ps);
+        const f32x4 u = epi == EPI_SILU ? sum_planes_coh(rsP, off + 16, S, ps) : a;
+        hsq = finish(m, n, a, u);
+      }
+      if (norm) lds[it] = hsq;
+    }
+  } else {
+    // UR items per thread and pass, the plane loads of all of them issued before adding (PB planes at a time, at
+    // most 16 loads in flight): a round trip per PB planes rather than one per item; planes still summed in order
+    constexpr int PB = 16 / (2 * UR) > 0 ? 16 / (2 * UR) : 1;
+    for (int it0 = 0; it0 < nitem; it0 += UR * NT) {
+      f32x4 ag[UR], au[UR];
+      uint32_t off[UR];
+      bool live[UR];
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int it = it0 + u * NT + tid, mi = it / gpr, n = n0 + (it - mi * gpr) * gw, m = m0 + mi;
+        live[u] = it < nitem && m < M && n < N;
+        off[u] = live[u] ? (uint32_t)(((int64_t)m * N + n) * 4) : 0u;
+      }
+      for (int s0 = 0; s0 < S; s0 += PB) {
+        f32x4 cg[PB][UR], cu[PB][UR];
+#pragma unroll
+        for (int j = 0; j < PB; ++j)
+#pragma unroll
+          for (int u = 0; u < UR; ++u) {
+            const uint32_t o = (uint32_t)(off[u] + (int64_t)min(s0 + j, S - 1) * ps * 4);
+            cg[j][u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsP, o, 0, kCoh));
+            if (epi == EPI_SILU)
+              cu[j][u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rsP, o + 16, 0, kCoh));
+          }
+#pragma unroll
+        for (int j = 0; j < PB; ++j)
+#pragma unroll
+          for (int u = 0; u < UR; ++u) {
+            if (s0 + j >= S) continue;
+            ag[u] = s0 + j == 0 ? cg[j][u] : ag[u] + cg[j][u];
+            if (epi == EPI_SILU) au[u] = s0 + j == 0 ? cu[j][u] : au[u] + cu[j][u];
+          }
+      }
+#pragma unroll
+      for (int u = 0; u < UR; ++u) {
+        const int it = it0 + u * NT + tid, mi = it / gpr, n = n0 + (it - mi * gpr) * gw, m = m0 + mi;
+        const float hsq = live[u] ? finish(m, n, ag[u], epi == EPI_SILU ? au[u] : ag[u]) : 0.f;
+        if (norm && it < nitem) lds[it] = hsq;
+      }
+    }
   }
   if (!norm) return;
   // the tile's row sums of h^2, in column order

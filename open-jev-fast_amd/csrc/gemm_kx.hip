@@ -406,7 +406,8 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
         if (m < p.M && n < p.N)
           __builtin_amdgcn_raw_buffer_store_b128(v, rsP, (uint32_t)((zo + (int64_t)m * p.N + n) * 4), 0, kCoh);
       }
-      ol_epilogue<BN, BM, 512>(p, EPI, tn, tm, reinterpret_cast<float*>(smem));
+      // items batched per thread where the tile is small enough to keep the loads in registers
+      ol_epilogue<BN, BM, 512, (BN * BM <= 144 * 128 ? 4 : 2)>(p, EPI, tn, tm, reinterpret_cast<float*>(smem));
       return;
     }
   }
