@@ -127,14 +127,15 @@ hipError_t launch_fullattn_prep(const uint16_t* proj, int64_t N, int HQ, int HKV
 // Products of two bf16 values are exact in fp32, so the conv's sum order is the only one that fixes its bits; it is
 // kept. The head sums of squares are added in another order than the reference's (one rounding step at most).
 //
-// Work layout: one workgroup of 16 waves (1024 lanes) per packed row, grid = N rows + the padding groups.
+// Work layout: one workgroup of 8 waves (kLinThreads = 512 lanes) per packed row, grid = N rows + the padding
+// groups.
 //   1. conv + SiLU for all C channels (8 per lane per step, the four history rows and the 64 weight bytes as 16-byte
-//      loads; 10240 channels take 1.25 steps), the bf16 results kept in an LDS copy of the row;
+//      loads; 10240 channels take 2.5 steps), the bf16 results kept in an LDS copy of the row;
 //   2. one q/k head per wave at a time, 2 channels per lane: wave-total sum of squares, scaled in place in LDS;
 //      lanes below HV compute the gates into LDS meanwhile;
 //   3. the finished row is written slot after slot: every 16-byte chunk of a slot's q | k | v row is one lane's
 //      LDS read and global store, so each slot row goes out as one contiguous sweep; slot ids come in through
-//      LDS, 1024 at a time.
+//      LDS, kLinThreads at a time (the first batch fetched before step 1).
 // A padding group (the workgroups after the N row workgroups) writes zero rows to kPadSlots consecutive
 // padding slots.
 constexpr int kPadSlots = 8;
