@@ -81,7 +81,10 @@ def test_unpack_inverts_pack(O):
 # --------------------------------------------------------------------------------------- every plan-table row
 @pytest.mark.parametrize("M,N,K,kind", plan_rows(), ids=lambda v: str(v))
 def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
-    """Rows of kind | 4 are plans for packed weights: the call goes through the *_pk entry point."""
+    """Rows of kind | 4 are plans for packed weights: the call goes through the *_pk entry point. Sampled rows and
+    columns are checked against the oracle on the CPU; every element against the library's family-0 tile and
+    against the oracle's own arithmetic run on the GPU tensors (torch fp32 GEMM, an implementation independent of
+    this library)."""
     plan = pkg._lib.plan(M, N, K, kind)
     _say(f"case plan row M={M} N={N} K={K} kind={kind} plan={plan}")
     packed = bool(kind & 4)
@@ -103,6 +106,7 @@ def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
         ref = O.linear_bf16(xs, w[cols.to(dev)].cpu())
         _assert_tol(O, y[mrows.to(dev)][:, cols.to(dev)], ref, "sampled vs oracle")
         _assert_tol(O, y, ext.mm(x, w, cfg=ref_cfg), "every element vs the family-0 tile")
+        _assert_tol(O, y, O.linear_bf16(x, w), "every element vs the oracle (its fp32 GEMM run on the GPU)")
     elif kind == 1:
         I = N // 2
         out = mm_silu(x, wk)
@@ -112,6 +116,7 @@ def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
         ref = O.gate_up_silu(xs, gate[cols.to(dev)].cpu(), up[cols.to(dev)].cpu())
         _assert_tol(O, out[mrows.to(dev)][:, cols.to(dev)], ref, "sampled vs oracle")
         _assert_tol(O, out, ext.mm_silu_mul(x, w, cfg=ref_cfg), "every element vs the family-0 tile")
+        _assert_tol(O, out, O.gate_up_silu(x, gate, up), "every element vs the oracle (on the GPU)")
     else:
         res = torch.randn(M, N, generator=gx, device=dev).bfloat16()
         w1 = (1.0 + 0.1 * torch.randn(N, generator=gx, device=dev)).float()
@@ -123,6 +128,9 @@ def test_plan_table_row_full_size(pkg, ext, O, dev, M, N, K, kind):
         h2, hn2 = ext.mm_residual_rmsnorm(res, x, w, w1, mask, 1e-6, cfg=ref_cfg)
         _assert_tol(O, h, h2, "h every element vs the family-0 tile")
         _assert_tol(O, hn, hn2, "hn every element vs the family-0 tile")
+        rh_all, rhn_all = O.residual_proj(res, x, w, w1, mask, 1e-6)
+        _assert_tol(O, h, rh_all, "h every element vs the oracle (on the GPU)")
+        _assert_tol(O, hn, rhn_all, "hn every element vs the oracle (on the GPU)")
         assert int(hn[mask == 0].count_nonzero()) == 0, "masked rows of hn must be zero"
     torch.cuda.synchronize()
 
