@@ -179,3 +179,56 @@ def test_python_mirror_errors_without_gpu(pkg):
     assert n >= 1 and lt.lt2_info(h, 0)[1] == 2
     raw = lt.lt2_raw(h, 0)
     assert lt.lt2_add_raw(h, raw) == n
+
+
+def test_unsplit_weight_argument_validation(pkg):
+    L = pkg._lib.lib()
+    buf = ctypes.create_string_buffer(1 << 12)
+    p = ctypes.cast(ctypes.addressof(buf) + (-ctypes.addressof(buf)) % 16, ctypes.c_void_p)
+    assert L.ojx_unsplit_weight(p, p, 64, 96, 5, None) == 2  # K % S != 0
+    assert b"multiple of S" in L.ojx_last_error()
+    assert L.ojx_unsplit_weight(p, p, 60, 96, 2, None) == 2  # N not a multiple of 8
+    assert L.ojx_unsplit_weight(None, p, 64, 96, 2, None) == 1
+    assert L.ojx_unsplit_weight(p, ctypes.c_void_p(p.value + 2), 64, 96, 2, None) == 1
+
+
+C_HOST = r"""
+#include <stdio.h>
+#include "ojx.h"
+int main(void) {
+  ojx_cfg c;
+  if (ojx_plan(288, 34816, 5120, OJX_KIND_SILU_MUL | OJX_KIND_PACKED, &c) != OJX_OK) return 1;
+  long long ws = (long long)ojx_workspace_bytes(288, 34816, 5120, OJX_KIND_SILU_MUL | OJX_KIND_PACKED, &c);
+  printf("%s|%d|%d|%d|%lld\n", ojx_version(), ojx_num_tiles(), c.tile, c.splitk, ws);
+  return ws < 0;
+}
+"""
+
+
+def test_c_host_compiles_links_and_plans(pkg, tmp_path):
+    """include/ojx.h is plain C (C99) and C++; a C host links libojx.so and uses its host-side calls (the plan
+    lookup and workspace size need no GPU), as the C / C++ integration path does."""
+    import shutil
+    import subprocess
+    inc = os.path.join(ROOT, "include")
+    for comp, std, lang in (("gcc", "-std=c99", "c"), ("g++", "-std=c++17", "c++")):
+        if shutil.which(comp) is None:
+            pytest.skip(f"{comp} not installed")
+        r = subprocess.run([comp, std, "-Wall", "-Werror", "-fsyntax-only", "-x", lang, os.path.join(inc, "ojx.h")],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+    src = tmp_path / "host.c"
+    src.write_text(C_HOST)
+    exe = tmp_path / "host"
+    libdir = os.path.dirname(pkg._lib.LIB_PATH)
+    r = subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", inc, str(src), "-o", str(exe), pkg._lib.LIB_PATH,
+                        "-Wl,-rpath," + libdir, "-Wl,--allow-shlib-undefined"], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    version, ntiles, tile, splitk, ws = r.stdout.strip().split("|")
+    c = pkg._lib.plan(288, 34816, 5120, 1 | 4)
+    assert version == pkg._lib.lib().ojx_version().decode()
+    assert int(ntiles) == pkg._lib.lib().ojx_num_tiles()
+    assert (int(tile), int(splitk)) == (c.tile, c.splitk)
+    assert int(ws) == pkg._lib.workspace_bytes(288, 34816, 5120, 1 | 4)
