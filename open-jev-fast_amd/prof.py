@@ -3,7 +3,8 @@
     rocprofv3 --kernel-trace --stats -d /tmp/prof -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
     rocprofv3 --pmc FETCH_SIZE -d /tmp/pmc -- python3 open-jev-fast_amd/prof.py --shape gate_up --m 288
     python3 open-jev-fast_amd/prof.py --copy-mb 512     # plain copy kernel, to calibrate FETCH_SIZE / WRITE_SIZE
-    (--packed: weights in the packed layout of ext.pack_weight, the layout bench.py uses by default)
+    (--packed: weights in the packed layout of ext.pack_weight, the layout bench.py uses by default; --zero-w:
+    all-zero weights, to see how much of a kernel's time depends on the operands' values)
 
 Shapes are those of open_jev_fast_amd.perf.SHAPES (plus any --n/--k override); weights rotate over copies larger
 than the Infinity Cache so each call streams its weights from HBM.
@@ -30,6 +31,8 @@ def main():
     ap.add_argument("--calls", type=int, default=40)
     ap.add_argument("--copy-mb", type=int, default=0)
     ap.add_argument("--packed", action="store_true", help="weights in the packed layout (ext.pack_weight)")
+    ap.add_argument("--zero-w", action="store_true", help="all-zero weights: the same data movement and MFMA "
+                    "count with operands that draw less power (the clock's dependence on the data)")
     args = ap.parse_args()
     if args.copy_mb:
         n = args.copy_mb << 20
@@ -50,7 +53,8 @@ def main():
     M = args.m
     cfg = pkg._lib.cfg(args.tile, args.splitk, one_launch=args.one_launch) if args.tile >= 0 else None
     x = torch.randn(M, K, device="cuda").bfloat16()
-    ws = [(torch.randn(N, K, device="cuda") * 0.02).bfloat16() for _ in range(perf.copies_for(N * K * 2))]
+    ws = [(torch.randn(N, K, device="cuda") * (0.0 if args.zero_w else 0.02)).bfloat16()
+          for _ in range(perf.copies_for(N * K * 2))]
     if args.packed:
         ws = [ext.pack_weight(w) for w in ws]
     res = torch.randn(M, N, device="cuda").bfloat16()
