@@ -231,6 +231,16 @@ def test_unsplit_weight_layout(pkg, ext, dev, N, K, S):
     assert u2 is not u and torch.equal(u2, w * 2)
     with pytest.raises(RuntimeError, match="multiples of 8"):
         ext.unsplit_weight(torch.zeros(2, 8, 12, dtype=torch.bfloat16, device=dev))
+    if N * K <= 1 << 20:  # first seen inside a graph capture: made by the graph, not kept
+        wsk3 = (w * 3).view(N, S, K // S).permute(1, 2, 0).contiguous()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            u3 = ext.unsplit_weight(wsk3)
+        for _ in range(3):
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(u3, w * 3)
+        assert ext.unsplit_weight(wsk3) is not u3 and torch.equal(ext.unsplit_weight(wsk3), w * 3)
 
 
 # ----------------------------------------------------------------------------------------------- epilogues
