@@ -964,6 +964,8 @@ static const TileEntry kTiles[] = {
     OJX_KX(16, 1, 0),               // 89 256 x 64
     OJX_TILE(32, 16, 128, 2, 1),    // 90 skinny M, 32 W rows: N / 32 workgroups without split-K
     OJX_TILE(32, 16, 256, 2, 1),    // 91 the same, deeper K stages
+    OJX_KX(10, 4, 0),               // 92 160 x 256: N = 5120 in 32 W tiles, 256 tiles at M = 2048
+    OJX_KX(10, 2, 0),               // 93 160 x 128: 256 tiles at M = 1024
 };
 
 static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];

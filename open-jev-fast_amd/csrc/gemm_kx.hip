@@ -473,5 +473,7 @@ template __global__ void gemm_kx_kernel<8, 2, 0>(const GemmParams, const int);  
 template __global__ void gemm_kx_kernel<8, 1, 0>(const GemmParams, const int);  // 128 x 64
 template __global__ void gemm_kx_kernel<16, 2, 0>(const GemmParams, const int);  // 256 x 128: one head per tile
 template __global__ void gemm_kx_kernel<16, 1, 0>(const GemmParams, const int);  // 256 x 64
+template __global__ void gemm_kx_kernel<10, 4, 0>(const GemmParams, const int);  // 160 x 256
+template __global__ void gemm_kx_kernel<10, 2, 0>(const GemmParams, const int);  // 160 x 128
 
 }  // namespace ojx
