@@ -23,7 +23,7 @@ class OjxCfg(ctypes.Structure):
 
     def __repr__(self):
         t = f", tail {self.tail_rows} rows: tile {self.tail_tile} S {self.tail_splitk}" if self.tail_rows else ""
-        o = ", one launch" if self.one_launch else ""
+        o = {0: "", 1: ", one launch", 2: ", one launch + RMSNorm"}.get(self.one_launch, f", one_launch {self.one_launch}")
         return f"OjxCfg(tile {self.tile}, S {self.splitk}{t}{o})"
 
 

@@ -258,28 +258,28 @@ __device__ __forceinline__ void ol_epilogue(const GemmParams& p, const int epi, 
   // the tile's row sums of h^2, in column order
   __syncthreads();
   const __amdgpu_buffer_rsrc_t rsS = make_rsrc(p.ol_ss, (int64_t)p.tiles_n * M * 4);
-  if (tid < BM && m0 + tid < M) {
+  for (int r = tid; r < BM && m0 + r < M; r += NT) {  // a tile may have more rows than threads (BM > NT)
     float s = 0.f;
-    for (int c = 0; c < gpr; ++c) s += lds[tid * gpr + c];
-    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s), rsS, (uint32_t)(((int64_t)tn * M + m0 + tid) * 4), 0, kCoh);
+    for (int c = 0; c < gpr; ++c) s += lds[r * gpr + c];
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, s), rsS, (uint32_t)(((int64_t)tn * M + m0 + r) * 4), 0, kCoh);
   }
   if (!ol_arrive(p.ol_blocks + tm, (uint32_t)p.tiles_n)) return;
   // the block's row pass over all N columns
   float* rr = lds;  // [BM] 1 / rms
-  if (tid < BM && m0 + tid < M) {
+  for (int r = tid; r < BM && m0 + r < M; r += NT) {
     float s = 0.f;
     for (int t0 = 0; t0 < p.tiles_n; t0 += 16) {  // 16 loads in flight, added in tile order
       float v[16];
 #pragma unroll
       for (int u = 0; u < 16; ++u)
         v[u] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                             rsS, (uint32_t)(((int64_t)min(t0 + u, p.tiles_n - 1) * M + m0 + tid) * 4),
+                                             rsS, (uint32_t)(((int64_t)min(t0 + u, p.tiles_n - 1) * M + m0 + r) * 4),
                                              0, kCoh));
 #pragma unroll
       for (int u = 0; u < 16; ++u)
         if (t0 + u < p.tiles_n) s += v[u];
     }
-    rr[tid] = rsqrtf(s / (float)N + p.eps);
+    rr[r] = rsqrtf(s / (float)N + p.eps);
   }
   __syncthreads();
   // 8 items (8 columns each) per thread per batch: the h loads of a batch go out together

@@ -7,7 +7,8 @@ add_rmsnorm_sk2 launch, src/kernels.cu:1444-1501, src/fastmodel.py:196-203). Che
 * y (plain), out (SiLU.mul), h and hn (residual, one_launch = 1) equal the two-launch path with the same tile and
   split bit for bit (the same sums in the same order); under one_launch = 2, hn within one bf16 rounding step (its
   sum of squares is added in another order) and mostly equal; masked rows zero;
-* row-major and packed weights, ragged M / N / K (M over several M tiles too), splits 2 .. 16;
+* row-major and packed weights, ragged M / N / K (M over several M tiles too, and past 256 rows in the
+  288-row tiles, whose 256 threads each take more than one row of the RMSNorm pass), splits 2 .. 16;
 * back-to-back calls and HIP graph replays (the arrival counters re-arm themselves);
 * the north star's tolerance against the oracle at full size (o_proj, down, QKV, gate-up at M = 1 / 7 / 16).
 """
@@ -46,7 +47,8 @@ def _inputs(M, N, K, seed, dev):
     return x, w, res, w1, mask
 
 
-@pytest.mark.parametrize("M,N,K", [(1, 1040, 640), (7, 264, 1024), (16, 528, 768), (37, 1040, 1152), (150, 1040, 1152)])
+@pytest.mark.parametrize("M,N,K", [(1, 1040, 640), (7, 264, 1024), (16, 528, 768), (37, 1040, 1152), (150, 1040, 1152),
+                                   (300, 264, 1024)])
 @pytest.mark.parametrize("packed", [False, True])
 def test_one_launch_equals_two_launches(pkg, ext, dev, M, N, K, packed):
     x, w, res, w1, mask = _inputs(M, N, K, M + N + K, dev)
