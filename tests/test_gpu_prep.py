@@ -204,3 +204,61 @@ def test_linattn_prep_rejects(ext, dev):
         a2 = list(args)
         a2[10] = 8
         ext.linattn_prep_dedup2(*a2, 128, True)
+
+
+# ---------------------------------------------------------------- seeded random cases
+def _random_prep_cases(n=30):
+    import numpy as np
+    rng = np.random.default_rng(7)
+    full, lin = [], []
+    for i in range(n):
+        RD = int(rng.choice([16, 32, 64, 128, 256]))
+        full.append((i, int(rng.integers(1, 300)), int(rng.integers(1, 9)), int(rng.integers(1, 5)), RD))
+        ng = int(rng.integers(1, 4))
+        nl = int(rng.integers(1, 7))
+        tree = (int(rng.integers(1, 60)), [int(v) for v in rng.integers(0, 11, ng)],
+                [int(v) for v in rng.integers(0, ng, nl)], [int(v) for v in rng.integers(1, 9, nl)])
+        HK = int(rng.choice([1, 2, 4]))
+        lin.append((i, tree, HK, bool(rng.integers(0, 2))))
+    return full, lin
+
+
+_RFULL, _RLIN = _random_prep_cases()
+
+
+@pytest.mark.parametrize("case", _RFULL, ids=lambda c: f"f{c[0]}-N{c[1]}-q{c[2]}-kv{c[3]}-rd{c[4]}")
+def test_fullattn_prep_random(ext, O, dev, case):
+    i, N, HQ, HKV, RD = case
+    D = 256
+    _say(f"case prep random {i}: N={N} HQ={HQ} HKV={HKV} RD={RD}")
+    proj, qw1, kw1, cos, sin = _inputs(N, HQ, HKV, D, RD, seed=1000 + i)
+    qt, kt, vt, gate = ext.fullattn_prep2(proj.to(dev), qw1.to(dev), kw1.to(dev), cos.to(dev), sin.to(dev), 1, N,
+                                          HQ, HKV, D, EPS)
+    torch.cuda.synchronize()
+    rq, rk, rv, rg = O.fullattn_prep(proj, qw1, kw1, cos, sin, HQ, HKV, D, EPS)
+    assert torch.equal(vt[0].cpu(), rv) and torch.equal(gate.cpu(), rg)
+    _close_bf16(qt[0], rq, "q")
+    _close_bf16(kt[0], rk, "k")
+
+
+@pytest.mark.parametrize("case", _RLIN, ids=lambda c: f"l{c[0]}-hk{c[2]}-rq{int(c[3])}")
+def test_linattn_prep_random_trees(ext, dev, case):
+    i, tree, HK, rep_qk = case
+    HV = 3 * HK
+    _say(f"case linattn_prep random {i}: tree={tree} HK={HK} rep_qk={rep_qk}")
+    LO, lay, proj, convw, A_log, dt_bias, KD, VD = _lin_inputs(tree, HK, HV, seed=2000 + i)
+    d = lambda a: torch.as_tensor(a).to(dev).contiguous()  # noqa: E731
+    q, k, v, g, beta = ext.linattn_prep_dedup2(proj.to(dev), d(lay["hist"]), d(lay["rep_ptr"]), d(lay["rep_pos"]),
+                                               lay["L2"], convw.to(dev), A_log.to(dev), dt_bias.to(dev), KD, VD, HV,
+                                               HK, 128, rep_qk)
+    torch.cuda.synchronize()
+    rq_, rk_, rv_, rg_, rb_ = LO.linattn_prep(proj, lay["hist"], lay["rep_ptr"], lay["rep_pos"], lay["L2"], convw,
+                                              A_log, dt_bias, KD, VD, HV, HK, 128, rep_qk)
+    _ulp_close(v, rv_, "v", min_equal=0.98)
+    _ulp_close(q, rq_, "q", steps=2, min_equal=0.98)
+    _ulp_close(k, rk_, "k", steps=2, min_equal=0.98)
+    _ulp_close(beta, rb_, "beta", min_equal=0.98)
+    assert torch.allclose(g.cpu(), rg_, rtol=2e-6, atol=0), (g.cpu() - rg_).abs().max()
+    pad = torch.as_tensor(lay["src"].reshape(-1) < 0)
+    for tnsr in (q, k, v, g, beta):
+        assert bool((tnsr.cpu()[pad] == 0).all())
