@@ -98,7 +98,7 @@ SkPlan sk_plan(const ojx::TileInfo* t, int64_t M, int64_t N, int64_t K, int32_t 
 }
 
 bool part_fits(int64_t K, int32_t tile, int32_t splitk) {
-  if (tile < 0 || tile >= ojx::num_tiles()) return false;
+  if (tile < 0 || tile >= ojx::num_tiles() || ojx::tile_info(tile)->family < 0) return false;  // < 0: retired id
   if (splitk < 1 || splitk > kMaxSplit) return false;
   if (is_sk(tile)) return true;  // splitk is the stream-K spread there, not a K split
   const int64_t ch = kchunk_for(K, splitk);

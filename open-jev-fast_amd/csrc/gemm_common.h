@@ -26,49 +26,7 @@ __device__ __forceinline__ uint4 bload_nt(__amdgpu_buffer_rsrc_t r, uint32_t off
 }
 constexpr uint32_t kOOB = 0x80000000u;  // an offset past every descriptor's range: the load returns zeros
 
-// The same descriptor as four dwords, for loads issued from inline assembly. The compiler's wait-count pass does
-// not track those loads; the kernel that uses them waits for them itself with an explicit s_waitcnt vmcnt(N),
-// where N counts the loads it issued after them. (Untracked loads only ever make the compiler's own waits on its
-// tracked loads stricter, never looser.)
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ u32x4 make_rsrc4(const void* base, int64_t bytes) {
-  const int32_t n = bytes > 0x7fffffffLL ? 0x7fffffff : (int32_t)(bytes < 0 ? 0 : bytes);
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  u32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  r[1] = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32) & 0xffffu);  // stride 0
-  r[2] = __builtin_amdgcn_readfirstlane((uint32_t)n);
-  r[3] = 0x00020000u;
-  return r;
-}
-__device__ __forceinline__ u32x4 bload_asm(const u32x4& r, uint32_t off) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=v"(v) : "v"(off), "s"(r) : "memory");
-  return v;
-}
-__device__ __forceinline__ u32x4 bload_asm_nt(const u32x4& r, uint32_t off) {  // with the non-temporal hint
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen nt" : "=v"(v) : "v"(off), "s"(r) : "memory");
-  return v;
-}
-// The same loads with a wave-uniform byte offset in soffset (an SGPR) added to the lane's offset.
-__device__ __forceinline__ u32x4 bload_asm_s(const u32x4& r, uint32_t off, uint32_t soff) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(off), "s"(r), "s"(soff) : "memory");
-  return v;
-}
-__device__ __forceinline__ u32x4 bload_asm_nt_s(const u32x4& r, uint32_t off, uint32_t soff) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(off), "s"(r), "s"(soff) : "memory");
-  return v;
-}
-// Same load into accumulation registers (AGPRs): used for data that only goes on to LDS, so the compiler never has
-// a reason to copy or spill it before the explicit wait (it cannot tell that the load is still in flight).
-__device__ __forceinline__ u32x4 bload_asm_agpr(const u32x4& r, uint32_t off) {
-  u32x4 v;
-  asm volatile("buffer_load_dwordx4 %0, %1, %2, 0 offen" : "=a"(v) : "v"(off), "s"(r) : "memory");
-  return v;
-}
+// Wait until at most N of this wave's vector-memory operations are outstanding (LDS-DMA loads, coherent stores).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");

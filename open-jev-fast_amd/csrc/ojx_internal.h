@@ -109,11 +109,9 @@ struct TileInfo {
   int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M
   int threads;
   int lds_bytes;
-  int family;  // 0: both operands through LDS; 1: W streamed straight into registers, x through LDS; 2: LDS DMA;
-               // 3: 32x32 MFMA, W streamed, x staged through registers; 4: 32x32 MFMA, W streamed, x by DMA;
-               // 5: persistent, 2 waves per SIMD, whole-tile waves then stream-K over the remainder;
-               // 6: K-interleaved wave pairs (both waves of a SIMD own the same fragments, alternate 32-k halves);
-               // 7: skinny weight streaming, operands straight into registers, K split over the waves
+  int family;  // 0: both operands through LDS; 5: persistent, 2 waves per SIMD, whole-tile waves then stream-K
+               // over the remainder; 6: K-interleaved wave pairs (both waves of a SIMD own the same fragments,
+               // alternate 32-k halves); -1: a retired id (1-4 were W-direct, LDS-DMA and 32x32-MFMA tiles)
 };
 
 // Tile registry (gemm.hip)

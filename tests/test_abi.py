@@ -32,10 +32,16 @@ def test_version_and_tiles(pkg):
     assert L.ojx_version().decode().endswith("src:" + build.source_digest())
     n = L.ojx_num_tiles()
     assert n >= 8
+    live = 0
     for t in range(n):
         info = pkg._lib.tile_info(t)
+        if info["family"] < 0:  # a retired id: never planned, fitted or launched
+            assert all(c.tile != t for c in pkg._lib.candidates(288, 1024, 2048, 0))
+            continue
+        live += 1
         assert info["bn"] % 16 == 0 and info["bm"] % 16 == 0 and info["bk"] % 32 == 0
         assert info["threads"] == 64 * info["wn"] * info["wm"]
+    assert live >= 8 and pkg._lib.tile_info(52)["family"] == -1
     with pytest.raises(RuntimeError, match="out of range"):
         pkg._lib.tile_info(n)
 

@@ -16,8 +16,8 @@ def _say(*a):
     print(*a, flush=True)
 
 
-def _tiles(pkg):
-    return range(pkg._lib.lib().ojx_num_tiles())
+def _tiles(pkg):  # the live tiles (a retired id reports family -1 and is never planned or launched)
+    return [t for t in range(pkg._lib.lib().ojx_num_tiles()) if pkg._lib.tile_info(t)["family"] >= 0]
 
 
 def _assert_tol(O, out, ref, what):
@@ -55,8 +55,8 @@ def test_mm_planned_and_f64(pkg, ext, O, dev, M, N, K):
 
 def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
     """Without split-K the tiles of one MFMA shape sum K in the same order: outputs are bit-identical across those
-    tiles and across runs (16x16x32 families 0-2 and 5; the 32x32x16 families 3-4 among themselves; the
-    K-interleaved family 6, which adds the sums of the even and odd 32-k blocks, among itself)."""
+    tiles and across runs (16x16x32 families 0 and 5; the K-interleaved family 6, which adds the sums of the even
+    and odd 32-k blocks, among itself)."""
     M, N, K = 96, 512, 1024
     x, w = O.seeded_inputs(M, N, K, seed=3)
     xd, wd = x.to(dev), w.to(dev)
@@ -64,13 +64,13 @@ def test_mm_tile_invariance_and_determinism(pkg, ext, O, dev):
     base = {}
     for t in _tiles(pkg):
         fam = pkg._lib.tile_info(t)["family"]
-        shape = 32 if fam in (3, 4) else "kx" if fam == 6 else 16
+        shape = "kx" if fam == 6 else 16
         y = ext.mm(xd, wd, cfg=(t, 1))
         if shape not in base:
             base[shape] = y
         assert torch.equal(y, base[shape]), f"tile {t}"
         assert torch.equal(y, ext.mm(xd, wd, cfg=(t, 1))), f"tile {t} not deterministic"
-    assert len(base) == 3
+    assert len(base) == 2
     for S in (2, 4):
         a = ext.mm(xd, wd, cfg=(6, S))
         assert torch.equal(a, ext.mm(xd, wd, cfg=(6, S))), "split-K not deterministic"
@@ -100,6 +100,8 @@ def test_mm_strided_and_errors(pkg, ext, O, dev):
     with pytest.raises(RuntimeError):
         ext.mm(x.to(dev), w.to(dev), cfg=(999, 1))
     with pytest.raises(RuntimeError):
+        ext.mm(x.to(dev), w.to(dev), cfg=(52, 2))  # a retired tile id
+    with pytest.raises(RuntimeError):
         ext.mm(x.to(dev).t(), w.to(dev))  # not contiguous
     y = ext.mm(torch.empty(0, 64, dtype=torch.bfloat16, device=dev), w.to(dev))
     assert y.shape == (0, 64)
@@ -114,21 +116,19 @@ def test_tail_configs(pkg, ext, O, dev, M):
     x, w = O.seeded_inputs(M, N, K, seed=M + 11)
     ref = O.linear_bf16(x, w)
     xd, wd = x.to(dev), w.to(dev)
-    for key in [(66, 1, 54, 1, 232), (14, 2, 0, 3, 488), (48, 1, 66, 2, 104), (6, 1, 6, 1, 8)]:
+    for key in [(6, 1, 4, 1, 232), (14, 2, 0, 3, 488), (10, 1, 2, 2, 104), (6, 1, 6, 1, 8)]:
         _say(f"case tail mm M={M} cfg={key}")
         y = ext.mm(xd, wd, cfg=key)
         _assert_tol(O, y, ref, f"cfg {key}")
         if key[1] == 1 and key[3] == 1:
-            fam = lambda t: pkg._lib.tile_info(t)["family"] in (3, 4)  # noqa: E731
-            if fam(key[0]) == fam(key[2]):
-                assert torch.equal(y, ext.mm(xd, wd, cfg=(key[0], 1))), f"cfg {key} not bit-identical"
+            assert torch.equal(y, ext.mm(xd, wd, cfg=(key[0], 1))), f"cfg {key} not bit-identical"
     I = 264
     g = torch.Generator().manual_seed(M)
     wg = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
     wu = (torch.randn(I, K, generator=g) * 0.02).bfloat16()
     ref = O.gate_up_silu(x, wg, wu)
     packed = ext.pack_gate_up(wg.to(dev), wu.to(dev))
-    for key in [(66, 1, 54, 1, 144), (14, 2, 49, 2, 16), (6, 1, 6, 1, 8)]:
+    for key in [(6, 1, 4, 1, 144), (14, 2, 10, 2, 16), (6, 1, 6, 1, 8)]:
         _say(f"case tail silu M={M} cfg={key}")
         out = ext.mm_silu_mul(xd, packed, cfg=key)
         _assert_tol(O, out, ref, f"cfg {key}")

@@ -16,7 +16,7 @@ N_CASES = int(__import__("os").environ.get("OJX_RANDOM_CASES", "160"))
 
 
 def _cases():
-    rng = np.random.default_rng(20261202)
+    rng = np.random.default_rng(int(__import__("os").environ.get("OJX_RANDOM_SEED", "20261202")))
     out = []
     for i in range(N_CASES):
         kind = int(rng.integers(0, 3))
