@@ -72,13 +72,13 @@ const char* ojx_version(void);
 int ojx_init(void);
 
 /* Tile registry: info7 = {BN (W rows), BM (x rows), BK, waves along N, waves along M, threads, family}.
- * Family: 0 both operands via LDS, 1 W streamed to registers, 2 LDS DMA (all 16x16x32 MFMA); 3 W streamed to
- * registers on 32x32x16 MFMA, 4 the same with x copied to LDS by DMA; 5 persistent (one workgroup per CU, two
- * waves per SIMD, LDS DMA, 16x16x32 MFMA): whole-tile waves, then the remaining tiles' K iterations spread over
- * the grid (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles);
- * split tiles are summed by a second, small launch.
- * Tiles of one MFMA shape sum K in the same order, so without split-K (stream-K spread 1 for family 5) they give
- * bit-identical results; across MFMA shapes results agree to fp32 rounding. Stream-K results are deterministic:
+ * Family (all on 16x16x32 MFMA): 0 both operands through registers into LDS; 5 persistent (one workgroup per CU,
+ * two waves per SIMD, LDS DMA): whole-tile waves, then the remaining tiles' K iterations spread over the grid
+ * (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles), split
+ * tiles summed by a second, small launch; 6 K-interleaved wave pairs (the two waves of a SIMD take alternate 32-k halves and add their sums at the end);
+ * -1 a retired id (ids 16-72), which no plan, candidate list or launch accepts.
+ * Tiles of families 0 and 5 sum K in the same order, so without split-K (stream-K spread 1 for family 5) they
+ * give bit-identical results; family 6 agrees with them to fp32 rounding. Stream-K results are deterministic:
  * the pieces of a tile are summed in K order whatever order they finish in. */
 int ojx_num_tiles(void);
 int ojx_tile_info(int32_t tile, int32_t* info7);
