@@ -76,7 +76,8 @@ int ojx_init(void);
  * two waves per SIMD, LDS DMA): whole-tile waves, then the remaining tiles' K iterations spread over the grid
  * (stream-K), with splitk = the most pieces one remaining tile is cut into on average (1 = whole tiles), split
  * tiles summed by a second, small launch; 6 K-interleaved wave pairs (the two waves of a SIMD take alternate
- * 32-k halves and add their sums at the end); -1 a retired id (ids 16-72), which no plan, candidate list or launch accepts.
+ * 32-k halves and add their sums at the end); -1 a retired id (ids 16-72), which no plan, candidate list or
+ * launch accepts.
  * Tiles of families 0 and 5 sum K in the same order, so without split-K (stream-K spread 1 for family 5) they
  * give bit-identical results; family 6 agrees with them to fp32 rounding. Stream-K results are deterministic:
  * the pieces of a tile are summed in K order whatever order they finish in. */
