@@ -50,12 +50,26 @@ SHAPES = [(M, N, K) for M in (1, 7, 16, 64, 128, 288, 539, 1024, 2048)
           for N, K in ((14336, 5120), (34816, 5120), (5120, 17408), (5120, 6144), (16384, 5120), (16480, 5120))]
 
 
-@pytest.mark.parametrize("kind", [0, 1, 2])
+def test_plan_table_names_live_tiles(pkg):
+    """Every tile id stored in the plan table (main and tail) is a live tile: a retired id reports family -1."""
+    import os
+    import re
+    src = os.path.join(os.path.dirname(pkg.__file__), "csrc", "plan_table.inc")
+    rows = [list(map(int, m.group(1).split(","))) for m in re.finditer(r"^\{([^}]*)\}", open(src).read(), re.M)]
+    assert len(rows) > 100
+    for r in rows:
+        for t in (r[4], r[6]):
+            assert pkg._lib.tile_info(t)["family"] >= 0, f"plan row {r} names tile {t}"
+
+
+@pytest.mark.parametrize("kind", [0, 1, 2, 4, 5, 6])
 def test_plan_valid_for_every_contract_shape(pkg, kind):
     L = pkg._lib.lib()
     for M, N, K in SHAPES:
         c = pkg._lib.plan(M, N, K, kind)
         assert 0 <= c.tile < L.ojx_num_tiles() and 1 <= c.splitk <= 16
+        live = lambda t: pkg._lib.tile_info(t)["family"] >= 0  # noqa: E731
+        assert live(c.tile) and (c.tail_rows == 0 or live(c.tail_tile))
         ws = pkg._lib.workspace_bytes(M, N, K, kind)
         # each launch's data one after the other: split-K planes (rounded up to 256 bytes) or, for the persistent
         # family, partial-tile slots (or nothing)
