@@ -7,6 +7,8 @@ fixed by the seed (the same cases on every run). A second, smaller set draws ful
 up to the model's projection sizes), where a tile's split-K or stream-K bookkeeping spans hundreds of workgroups;
 its comparison stays on the GPU.
 """
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -14,9 +16,9 @@ import torch
 pytestmark = pytest.mark.gpu
 
 TOL = dict(max_rel=1e-2, mean_abs_rms=1e-3)
-N_CASES = int(__import__("os").environ.get("OJX_RANDOM_CASES", "160"))
-N_LARGE = int(__import__("os").environ.get("OJX_RANDOM_LARGE_CASES", "24"))
-SEED = int(__import__("os").environ.get("OJX_RANDOM_SEED", "20261202"))
+N_CASES = int(os.environ.get("OJX_RANDOM_CASES", "160"))
+N_LARGE = int(os.environ.get("OJX_RANDOM_LARGE_CASES", "24"))
+SEED = int(os.environ.get("OJX_RANDOM_SEED", "20261202"))
 
 
 def _cases():
