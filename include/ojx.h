@@ -53,8 +53,10 @@ enum {
  * planes). one_launch = 2 (family 0, ojx_gemm_residual_rmsnorm): the RMSNorm too (the last tile of each row block
  * to finish normalises its rows): one launch instead of two. Results equal the two-launch path's bit for bit,
  * except hn under one_launch = 2, whose sum of squares is added in another order (one rounding step at most). The
- * arrival counters are the library's (zero at load, left zero by every call): one-launch calls that overlap in
- * time on one GPU race. */
+ * arrival counters are the library's (zero at load, left zero by every call), one set per stream for the first 8
+ * streams of a device that launch such a plan: calls on different streams (each with its own workspace) may
+ * overlap; streams past the 8th share sets, and overlapping calls on a shared set race, as do graph replays on a
+ * stream other than the capture stream. */
 typedef struct {
   int32_t tile;
   int32_t splitk;

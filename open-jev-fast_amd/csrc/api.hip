@@ -260,7 +260,7 @@ int gemm(const ojx_cfg& c, int epi, const void* x, int64_t ldx, const void* w, i
   p.ol_tiles = p.ol_blocks = nullptr;
   if (c.one_launch && c.splitk > 1) {
     if (ws == nullptr) return fail(OJX_ERR_WORKSPACE, "one-launch split-K plan needs a workspace");
-    const int rc = hip_check(ojx::ol_counters(&p.ol_tiles, &p.ol_blocks), "one-launch counters");
+    const int rc = hip_check(ojx::ol_counters(st, &p.ol_tiles, &p.ol_blocks), "one-launch counters");
     if (rc != OJX_OK) return rc;
     p.one_launch = c.one_launch;
     p.ol_parts = reinterpret_cast<float*>(static_cast<char*>(ws) + ws_off);

@@ -20,35 +20,53 @@
 //     range, so a W tile is fetched from HBM into that XCD's L2 once.
 #include "gemm_common.h"
 
+#include <mutex>
 #include <type_traits>
 
 namespace ojx {
 
 // ------------------------------------------------------------------------------------------------ one launch
 // Arrival counters of the one-launch split-K (ol_epilogue, gemm_common.h): zero when the library loads, and every
-// call leaves the counters it used at zero again (the last arrival re-arms its counter). Calls of one-launch plans
-// that run at the same time on one GPU (different streams) share them and race.
-__device__ uint32_t g_ol_tiles[kOlMaxTiles];
-__device__ uint32_t g_ol_blocks[kOlMaxBlocks];
+// call leaves the counters it used at zero again (the last arrival re-arms its counter). There are kOlSets sets per
+// device; each stream that launches a one-launch plan is given a set of its own, the first time it does, so calls
+// on different streams (each with its own workspace) may overlap. Streams beyond kOlSets on one device share sets
+// (chosen by the stream's handle), and calls that overlap on a shared set race; so do graph replays on a stream
+// other than the one they were captured on, which keep the capture stream's set.
+__device__ uint32_t g_ol_tiles[kOlSets * kOlMaxTiles];
+__device__ uint32_t g_ol_blocks[kOlSets * kOlMaxBlocks];
 
-// Device addresses of the counters on the current device (looked up once per device, with it current).
-hipError_t ol_counters(uint32_t** tiles, uint32_t** blocks) {
-  static uint32_t* cache[64][2];
+// Device addresses of the counters of `stream`'s set on the current device (the symbol looked up once per device,
+// with it current).
+hipError_t ol_counters(hipStream_t stream, uint32_t** tiles, uint32_t** blocks) {
+  constexpr int kDev = 64;
+  static std::mutex mu;
+  static uint32_t* base[kDev][2];
+  static hipStream_t owner[kDev][kOlSets];
+  static int owners[kDev];
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
-  if (cache[dev][0] == nullptr) {
+  if (dev < 0 || dev >= kDev) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (base[dev][0] == nullptr) {
     void* t = nullptr;
     void* b = nullptr;
     if ((e = hipGetSymbolAddress(&t, HIP_SYMBOL(g_ol_tiles))) != hipSuccess) return e;
     if ((e = hipGetSymbolAddress(&b, HIP_SYMBOL(g_ol_blocks))) != hipSuccess) return e;
     if (t == nullptr || b == nullptr) return hipErrorInvalidSymbol;
-    cache[dev][1] = static_cast<uint32_t*>(b);
-    cache[dev][0] = static_cast<uint32_t*>(t);
+    base[dev][1] = static_cast<uint32_t*>(b);
+    base[dev][0] = static_cast<uint32_t*>(t);
   }
-  *tiles = cache[dev][0];
-  *blocks = cache[dev][1];
+  int set = -1;
+  for (int i = 0; i < owners[dev] && set < 0; ++i)
+    if (owner[dev][i] == stream) set = i;
+  if (set < 0 && owners[dev] < kOlSets) {
+    set = owners[dev]++;
+    owner[dev][set] = stream;
+  }
+  if (set < 0) set = (int)((reinterpret_cast<uintptr_t>(stream) >> 4) % kOlSets);
+  *tiles = base[dev][0] + (size_t)set * kOlMaxTiles;
+  *blocks = base[dev][1] + (size_t)set * kOlMaxBlocks;
   return hipSuccess;
 }
 

@@ -94,16 +94,17 @@ struct GemmParams {
   // one-launch split-K (family 0, splits > 1): the fp32 planes, the split reduction with its epilogue and, for the
   // residual epilogue with hn, the rows' RMSNorm all run in the GEMM launch (see ol_epilogue in gemm.hip)
   int one_launch;                   // 1: reduction in the launch; 2: and the residual epilogue's RMSNorm (hn)
-  uint32_t* ol_tiles; uint32_t* ol_blocks;  // the library's arrival counters on this device (ol_counters)
+  uint32_t* ol_tiles; uint32_t* ol_blocks;  // the stream's set of the library's arrival counters (ol_counters)
   float* ol_parts;                  // [S, M, N] fp32 planes (workspace)
   float* ol_ss;                     // [tiles_n, M] fp32 sums of h^2 over each N tile's columns (workspace)
   const float* w1; const int32_t* rowmask; float eps;
   uint16_t* hn;                     // RMSNorm output [M, N] of the residual epilogue (null: h only)
 };
 
-// Arrival counters of the one-launch split-K (gemm.hip): per tile and per M block of a launch.
-constexpr int kOlMaxTiles = 16384, kOlMaxBlocks = 4096;
-hipError_t ol_counters(uint32_t** tiles, uint32_t** blocks);
+// Arrival counters of the one-launch split-K (gemm.hip): per tile and per M block of a launch, in kOlSets sets per
+// device, one per stream (streams beyond kOlSets share).
+constexpr int kOlMaxTiles = 16384, kOlMaxBlocks = 4096, kOlSets = 8;
+hipError_t ol_counters(hipStream_t stream, uint32_t** tiles, uint32_t** blocks);
 
 struct TileInfo {
   int bn, bm, bk, wn, wm;  // W rows, X rows, K depth, waves along N, waves along M

@@ -52,27 +52,28 @@ def _cfgp(cfg):
     return ctypes.byref(cfg)
 
 
-_WS = {}        # device index -> the workspace handed to eager calls and captures
+_WS = {}        # (device index, stream handle) -> the workspace handed to that stream's eager calls and captures
 _WS_KEEP = []   # every workspace a graph capture has used: kept alive for the life of the process
 
 
 def _workspace(M, N, K, kind, cfg, device):
     """Workspace of one call: split-K fp32 planes or stream-K partial tiles (scratch, contents irrelevant on entry).
 
-    One buffer per device is kept and grown as needed. A graph capture records the buffer's address, so a buffer
+    One buffer per stream of each device is kept and grown as needed, so calls on different streams may overlap (the
+    library gives each stream its own set of arrival counters for the one-launch plans too). A graph capture records the buffer's address, so a buffer
     that a capture has used is not freed while graphs may replay: when a later call needs a larger one, the old
     buffer moves to _WS_KEEP instead of going back to the caching allocator (where a replay would write into memory
     that other tensors may own by then). The larger buffer becomes the device's buffer for every later call,
-    eager or captured, so the kept memory grows only with the largest workspace seen, not with the number of
-    captures. release_workspaces() drops the kept buffers once the caller's graphs are gone.
-    Calls that run concurrently on different streams of one device would share the buffer: such callers pass a
-    workspace of their own through the C-ABI."""
+    eager or captured, so the kept memory grows only with the largest workspace seen per stream, not with the number
+    of captures. release_workspaces() drops the kept buffers once the caller's graphs are gone. A captured graph
+    replayed on another stream keeps the capture stream's workspace: replays that overlap with calls on the capture
+    stream race on it."""
     n = lib().ojx_workspace_bytes(M, N, K, kind, _cfgp(cfg))
     if n < 0:
         check(1)
     if n == 0:
         return None, 0
-    key = torch.device(device).index
+    key = (torch.device(device).index, torch.cuda.current_stream(device).cuda_stream)
     ws = _WS.get(key)
     capturing = torch.cuda.is_current_stream_capturing()
     if ws is not None and ws[0].numel() >= n:

@@ -156,3 +156,55 @@ def test_one_launch_full_size_vs_oracle(pkg, ext, O, dev, shape, M):
         for got, ref, nm in ((h, rh, "h"), (hn, rhn, "hn")):
             ok, a, b = O.tolerance_ok(got.float().cpu(), ref.float(), **TOL)
             assert ok, (nm, a, b)
+
+
+def test_one_launch_plans_on_concurrent_streams(pkg, ext, dev):
+    """Four streams run one-launch plans at the same time: each stream's 24 calls are captured in a HIP graph on that
+    stream, and the four graphs are replayed together, so their kernels overlap on the GPU. Each stream has its own
+    set of the library's arrival counters (and ext its own workspace), so every result equals the same call run
+    alone, bit for bit, on every replay. Plain (families 0 and 6) and residual with the RMSNorm fold."""
+    L = pkg._lib
+    shapes = [(64, 2048, 4096, 0, 0), (64, 4096, 2048, 0, 6), (128, 1024, 4096, 2, 0), (7, 3072, 3072, 0, 0)]
+    calls = []
+    for i, (M, N, K, kind, fam) in enumerate(shapes):
+        x, w, res, w1, mask = _inputs(M, N, K, 100 + i, dev)
+        ol = 2 if kind == 2 else 1
+        cfg = next(c for c in L.candidates(M, N, K, kind)
+                   if c.one_launch == ol and c.splitk >= 3 and L.tile_info(c.tile)["family"] == fam)
+        if kind == 2:
+            calls.append((f"residual {M}x{N}x{K} {cfg}",
+                          lambda x=x, w=w, res=res, w1=w1, mask=mask, cfg=cfg:
+                          torch.cat(ext.mm_residual_rmsnorm(res, x, w, w1, mask, 1e-6, cfg=cfg), 1)))
+        else:
+            calls.append((f"plain {M}x{N}x{K} {cfg}", lambda x=x, w=w, cfg=cfg: ext.mm(x, w, cfg=cfg)))
+    alone = []
+    for what, f in calls:
+        _say(f"case streams alone {what}")
+        alone.append(f())
+        torch.cuda.synchronize()
+    streams = [torch.cuda.Stream(device=dev) for _ in calls]
+    graphs, outs = [], []
+    for i, (what, f) in enumerate(calls):
+        _say(f"case streams capture {what}")
+        with torch.cuda.stream(streams[i]):
+            f()  # eager first on this stream: its workspace exists before the capture
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=streams[i]):
+            outs.append([f() for _ in range(24)])
+        graphs.append(g)
+    torch.cuda.synchronize()
+    for rep in range(3):
+        _say(f"case streams concurrent replay {rep}")
+        for o in outs:
+            for t in o:
+                t.zero_()
+        cur = torch.cuda.current_stream(dev)
+        for i, g in enumerate(graphs):
+            streams[i].wait_stream(cur)
+            with torch.cuda.stream(streams[i]):
+                g.replay()
+        torch.cuda.synchronize()
+        for i, (what, _) in enumerate(calls):
+            for r, o in enumerate(outs[i]):
+                assert torch.equal(o, alone[i]), f"{what}: replay {rep}, call {r} differs from the call run alone"
