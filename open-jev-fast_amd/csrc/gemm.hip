@@ -20,6 +20,7 @@
 //     range, so a W tile is fetched from HBM into that XCD's L2 once.
 #include "gemm_common.h"
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -337,7 +338,10 @@ static const TileEntry kTiles[] = {
     OJX_KX(10, 2, 0),               // 93 160 x 128: 256 tiles at M = 1024
 };
 
-static bool g_attr_set[sizeof(kTiles) / sizeof(kTiles[0])];
+// Per device (the attribute is set with the device current) and per tile; threads that race here both set the same
+// attribute, which is harmless.
+constexpr int kAttrDevices = 64;
+static std::atomic<bool> g_attr_set[kAttrDevices][sizeof(kTiles) / sizeof(kTiles[0])];
 
 int num_tiles() { return (int)(sizeof(kTiles) / sizeof(kTiles[0])); }
 
@@ -347,15 +351,17 @@ const TileInfo* tile_info(int tile) {
 }
 
 static hipError_t set_attr(int tile) {
-  if (g_attr_set[tile]) return hipSuccess;
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess) return err;
+  if (dev < 0 || dev >= kAttrDevices) return hipErrorInvalidDevice;
+  std::atomic<bool>& done = g_attr_set[dev][tile];
+  if (done.load(std::memory_order_acquire)) return hipSuccess;
   const TileEntry& e = kTiles[tile];
-  if (e.fn == nullptr || e.info.lds_bytes == 0) {  // retired id, or static LDS only
-    g_attr_set[tile] = true;
-    return hipSuccess;
-  }
-  hipError_t err = hipFuncSetAttribute(reinterpret_cast<const void*>(e.fn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, e.info.lds_bytes);
-  if (err == hipSuccess) g_attr_set[tile] = true;
+  if (e.fn != nullptr && e.info.lds_bytes != 0)  // not a retired id, and dynamic LDS
+    err = hipFuncSetAttribute(reinterpret_cast<const void*>(e.fn), hipFuncAttributeMaxDynamicSharedMemorySize,
+                              e.info.lds_bytes);
+  if (err == hipSuccess) done.store(true, std::memory_order_release);
   return err;
 }
 
