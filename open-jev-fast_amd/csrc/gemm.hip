@@ -235,10 +235,12 @@ struct TileEntry {
 // Retired ids (16-72: register-streamed W, LDS-DMA and 32x32-MFMA tiles, slower than families 0, 5 and 6 on every
 // measured shape): kept so that stored ids keep their meaning; nothing plans, fits or launches them.
 #define OJX_RETIRED {{0, 0, 0, 0, 0, 0, 0, -1}, nullptr}
-// K-interleaved pair tiles: BN = 16 FW W rows, BM = 16 (4 FX + XE) x rows, 8 waves, 64-k stages, two LDS buffers
-#define OJX_KX(FW, FX, XE)                                                                                   \
-  {{16 * FW, 16 * (4 * FX + XE), 64, 4, 2, 512, (3 * 16 * FW + 2 * 16 * (4 * FX + XE)) * 128, 6},           \
-   gemm_kx_kernel<FW, FX, XE>}
+// K-interleaved pair tiles: BN = 16 FW W rows, BM = 16 (4 FX + XE) x rows, 8 waves, 64-k stages; an x ring of XD
+// stages (the prefetch distance) and a W ring of XD + 1
+#define OJX_KXD(FW, FX, XE, XD)                                                                              \
+  {{16 * FW, 16 * (4 * FX + XE), 64, 4, 2, 512, ((XD + 1) * 16 * FW + XD * 16 * (4 * FX + XE)) * 128, 6},   \
+   gemm_kx_kernel<FW, FX, XE, XD>}
+#define OJX_KX(FW, FX, XE) OJX_KXD(FW, FX, XE, 2)
 
 // Order is the tile id used by the plan table; append only (ids are stored in plan_table.inc).
 static const TileEntry kTiles[] = {
@@ -336,6 +338,7 @@ static const TileEntry kTiles[] = {
     OJX_TILE(32, 16, 256, 2, 1),    // 91 the same, deeper K stages
     OJX_KX(10, 4, 0),               // 92 160 x 256: N = 5120 in 32 W tiles, 256 tiles at M = 2048
     OJX_KX(10, 2, 0),               // 93 160 x 128: 256 tiles at M = 1024
+    OJX_KXD(8, 1, 0, 4),            // 94 128 x 64, DMAs 4 stages ahead (weight streaming at M = 64-128)
 };
 
 // Per device (the attribute is set with the device current) and per tile; threads that race here both set the same

@@ -356,7 +356,7 @@ constexpr bool sk_asym(int BN, int BM) {
 constexpr int sk_lds(int BN, int BM) {
   return sk_asym(BN, BM) ? (3 * BN + 2 * BM) * 128 : sk_nbuf(BN, BM) * (BN + BM) * 128;
 }
-// K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves.
-template <int FW, int FX, int XE>
+// K-interleaved wave pairs (gemm_kx.hip): BN x BM = 16 FW x 16 (4 FX + XE), 8 waves, x ring of XD stages.
+template <int FW, int FX, int XE, int XD>
 __global__ void gemm_kx_kernel(const GemmParams p, const int epi);
 }  // namespace ojx

@@ -32,17 +32,20 @@ namespace {
 
 __device__ __forceinline__ void kx_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <int FW, int FX, int XE>
+template <int FW, int FX, int XE, int XD>
 struct KxShape {
   static constexpr int BN = 16 * FW, BM = 16 * (4 * FX + XE);
-  static constexpr int RB = 128, WD = 3;                          // W ring depth (stages of 64 k)
-  static constexpr int LDS = (WD * BN + 2 * BM) * RB;             // W ring + x double buffer
+  // x ring depth XD = the prefetch distance in stages of 64 k; the W ring has one stage more (a W slot is free as
+  // soon as its stage's W fragments are read, an x slot only once every wave holds its x fragments in registers)
+  static constexpr int RB = 128, WD = XD + 1;
+  static constexpr int LDS = (WD * BN + XD * BM) * RB;            // W ring + x ring
   static constexpr int NW = 8;
   static constexpr int EW = XE == 0 ? 0 : XE == 1 ? (FW + 3) / 4 : (FW + 1) / 2;  // extra W fragments per group
   static constexpr int NX = FX + (XE > 0 ? 1 : 0);                                  // x fragments per wave
   static constexpr int NACC = FW * FX + EW;                                         // accumulators per wave
   static constexpr int HF = (NACC + 1) / 2;                                         // fragments reduced by wave g
   static_assert(XE >= 0 && XE <= 2, "0..2 leftover x fragments");
+  static_assert(XD >= 2, "x ring of two stages or more");
   static_assert(4 * HF * 64 * 16 <= LDS, "the pair exchange must fit the stage buffers");
   static_assert(LDS <= 160 * 1024, "LDS");
 };
@@ -151,9 +154,9 @@ __device__ __forceinline__ void kx_fattn_epilogue(const GemmParams& p, f32x4 (&a
 
 // REV (two leftover x fragments only): the group walks its W fragments from the last one down, so that its extra
 // fragments (the upper half) come first; the other groups walk upwards. Either way the walk is static code.
-template <int FW, int FX, int XE, int EPI, bool REV, bool PK>
+template <int FW, int FX, int XE, int XD, int EPI, bool REV, bool PK>
 __device__ __forceinline__ void kx_body(const GemmParams& p) {
-  using S = KxShape<FW, FX, XE>;
+  using S = KxShape<FW, FX, XE, XD>;
   constexpr int BN = S::BN, BM = S::BM, RB = S::RB, NW = S::NW;
   // DMA waves: the waves that issue the operand DMAs. Only the second wave of each SIMD (h = 1) issues them, so a
   // wave stalled at a full texture-unit queue leaves its SIMD partner free to keep the MFMA pipe busy (measured
@@ -256,7 +259,7 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
     const uint32_t sx = (uint32_t)(st * BK * 2);  // kb is in the lane offsets
     const uint32_t sw = PK ? (uint32_t)(((kb >> 6) + st) * nbw * 2048) : sx;
     const __amdgpu_buffer_rsrc_t rX = ok ? rsX : rsNone, rW = ok ? rsW : rsNone;
-    uint8_t* const xd = xring + (st & 1) * XST;
+    uint8_t* const xd = xring + (st % XD) * XST;
     uint8_t* const wd = wring + (st % S::WD) * WST;
     const bool tail = ragged && st == nk - 1;  // rare
 #pragma unroll
@@ -299,17 +302,18 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   constexpr int H1 = GPW - NDG;               // issued after the barrier (H0 plus what does not fit the groups)
 
   bf16x8 xc[NX], wr[PD + 1];
+  static_assert((XD - 1) * GPW < 64, "DMA batches in flight must fit the vmcnt counter");
   if (nk > 0) {
-    dma(0, 0, GPW);
-    dma(1, 0, GPW);
-    if (dmaw) wait_vmcnt<GPW>();  // stage 0 has landed
+#pragma unroll
+    for (int st = 0; st < XD; ++st) dma(st, 0, GPW);
+    if (dmaw) wait_vmcnt<(XD - 1) * GPW>();  // stage 0 has landed
     kx_barrier();
 #pragma unroll
     for (int i = 0; i < NX; ++i) xc[i] = OJX_KX_RD(xring, xoff[i]);
 #pragma unroll
     for (int d = 0; d < PD; ++d) wr[d] = OJX_KX_RD(wring, woff[d]);
     kx_barrier();       // every wave holds its x fragments of stage 0: x slot 0 is free
-    dma(2, 0, H1);
+    dma(XD, 0, H1);
   }
   for (int t = 0; t < nk; ++t) {
     const uint8_t* sw = wring + (t % S::WD) * WST;
@@ -321,15 +325,15 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
       for (int i = 0; i < FX; ++i) acc[pp][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[i], acc[pp][i], 0, 0, 0);
       if constexpr (EW > 0)
         if (pp < EW) acce[pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[FX], acce[pp], 0, 0, 0);
-      if (pp < NDG) dma(t + 2, H1 + pp, H1 + pp + 1);
+      if (pp < NDG) dma(t + XD, H1 + pp, H1 + pp + 1);
     }
     bf16x8 xn[NX], wn[PD];
     const bool more = t + 1 < nk;
     if (more) {
-      if (dmaw) wait_vmcnt<GPW>();  // stage t+1 has landed (only the batch of stage t+2 may be outstanding)
+      if (dmaw) wait_vmcnt<(XD - 1) * GPW>();  // stage t+1 has landed (the batches of t+2 .. t+XD may not)
       kx_barrier();       // every wave's has, and every wave's W reads of stage t are done
       const uint8_t* nw = wring + ((t + 1) % S::WD) * WST;
-      const uint8_t* nx = xring + ((t + 1) & 1) * XST;
+      const uint8_t* nx = xring + ((t + 1) % XD) * XST;
 #pragma unroll
       for (int i = 0; i < NX; ++i) xn[i] = OJX_KX_RD(nx, xoff[i]);
 #pragma unroll
@@ -344,8 +348,8 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
         if (pp < EW) acce[pp] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, xc[FX], acce[pp], 0, 0, 0);
     }
     if (more) {
-      kx_barrier();       // every wave holds its x fragments of stage t+1: that x slot takes stage t+3
-      dma(t + 3, 0, H1);
+      kx_barrier();       // every wave holds its x fragments of stage t+1: that x slot takes stage t+1+XD
+      dma(t + 1 + XD, 0, H1);
 #pragma unroll
       for (int i = 0; i < NX; ++i) xc[i] = xn[i];
 #pragma unroll
@@ -436,44 +440,46 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
 
 }  // namespace
 
-template <int FW, int FX, int XE, int EPI>
+template <int FW, int FX, int XE, int XD, int EPI>
 __device__ __forceinline__ void kx_dir(const GemmParams& p) {
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (p.wpk) {
-    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true, true>(p);
-    else kx_body<FW, FX, XE, EPI, false, true>(p);
+    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, XD, EPI, true, true>(p);
+    else kx_body<FW, FX, XE, XD, EPI, false, true>(p);
   } else {
-    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, EPI, true, false>(p);
-    else kx_body<FW, FX, XE, EPI, false, false>(p);
+    if (XE == 2 && (wave & 1)) kx_body<FW, FX, XE, XD, EPI, true, false>(p);
+    else kx_body<FW, FX, XE, XD, EPI, false, false>(p);
   }
 }
 
-template <int FW, int FX, int XE>
+template <int FW, int FX, int XE, int XD>
 __global__ void __launch_bounds__(512) gemm_kx_kernel(const GemmParams p, const int epi) {
   if constexpr (FW == 16 && XE == 0) {  // the 256-row tiles also carry the full-attention prep epilogue
     if (epi == EPI_FATTN) {
-      kx_dir<FW, FX, XE, EPI_FATTN>(p);
+      kx_dir<FW, FX, XE, XD, EPI_FATTN>(p);
       return;
     }
   }
-  if (epi == EPI_SILU) kx_dir<FW, FX, XE, EPI_SILU>(p);
-  else if (epi == EPI_RESID) kx_dir<FW, FX, XE, EPI_RESID>(p);
-  else if (epi == EPI_F32) kx_dir<FW, FX, XE, EPI_F32>(p);
-  else kx_dir<FW, FX, XE, EPI_BF16>(p);
+  if (epi == EPI_SILU) kx_dir<FW, FX, XE, XD, EPI_SILU>(p);
+  else if (epi == EPI_RESID) kx_dir<FW, FX, XE, XD, EPI_RESID>(p);
+  else if (epi == EPI_F32) kx_dir<FW, FX, XE, XD, EPI_F32>(p);
+  else kx_dir<FW, FX, XE, XD, EPI_BF16>(p);
 }
 
 // Tile shapes of this family (registered in gemm.hip's tile table): BN x BM = 16 FW x 16 (4 FX + XE).
-template __global__ void gemm_kx_kernel<9, 4, 2>(const GemmParams, const int);  // 144 x 288
-template __global__ void gemm_kx_kernel<8, 4, 2>(const GemmParams, const int);  // 128 x 288
-template __global__ void gemm_kx_kernel<9, 2, 1>(const GemmParams, const int);  // 144 x 144
-template __global__ void gemm_kx_kernel<8, 4, 0>(const GemmParams, const int);  // 128 x 256
-template __global__ void gemm_kx_kernel<9, 1, 0>(const GemmParams, const int);  // 144 x 64
-template __global__ void gemm_kx_kernel<9, 2, 0>(const GemmParams, const int);  // 144 x 128
-template __global__ void gemm_kx_kernel<8, 2, 0>(const GemmParams, const int);  // 128 x 128
-template __global__ void gemm_kx_kernel<8, 1, 0>(const GemmParams, const int);  // 128 x 64
-template __global__ void gemm_kx_kernel<16, 2, 0>(const GemmParams, const int);  // 256 x 128: one head per tile
-template __global__ void gemm_kx_kernel<16, 1, 0>(const GemmParams, const int);  // 256 x 64
-template __global__ void gemm_kx_kernel<10, 4, 0>(const GemmParams, const int);  // 160 x 256
-template __global__ void gemm_kx_kernel<10, 2, 0>(const GemmParams, const int);  // 160 x 128
+template __global__ void gemm_kx_kernel<9, 4, 2, 2>(const GemmParams, const int);  // 144 x 288
+template __global__ void gemm_kx_kernel<8, 4, 2, 2>(const GemmParams, const int);  // 128 x 288
+template __global__ void gemm_kx_kernel<9, 2, 1, 2>(const GemmParams, const int);  // 144 x 144
+template __global__ void gemm_kx_kernel<8, 4, 0, 2>(const GemmParams, const int);  // 128 x 256
+template __global__ void gemm_kx_kernel<9, 1, 0, 2>(const GemmParams, const int);  // 144 x 64
+template __global__ void gemm_kx_kernel<9, 2, 0, 2>(const GemmParams, const int);  // 144 x 128
+template __global__ void gemm_kx_kernel<8, 2, 0, 2>(const GemmParams, const int);  // 128 x 128
+template __global__ void gemm_kx_kernel<8, 1, 0, 2>(const GemmParams, const int);  // 128 x 64
+template __global__ void gemm_kx_kernel<16, 2, 0, 2>(const GemmParams, const int);  // 256 x 128: one head per tile
+template __global__ void gemm_kx_kernel<16, 1, 0, 2>(const GemmParams, const int);  // 256 x 64
+template __global__ void gemm_kx_kernel<10, 4, 0, 2>(const GemmParams, const int);  // 160 x 256
+template __global__ void gemm_kx_kernel<10, 2, 0, 2>(const GemmParams, const int);  // 160 x 128
+// a deeper ring for the weight-streaming M = 64-128: twice the bytes in flight per CU
+template __global__ void gemm_kx_kernel<8, 1, 0, 4>(const GemmParams, const int);  // 128 x 64, 4 stages ahead
 
 }  // namespace ojx
