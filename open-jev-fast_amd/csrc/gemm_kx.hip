@@ -18,8 +18,10 @@
 //     so each wave then stores half of its group's outputs. The sum over k is (even 32-k blocks) + (odd 32-k
 //     blocks): deterministic, but a different rounding order from the other tile families.
 //   * Operands reach LDS by DMA (buffer_load ... lds, 16 B per lane, one 8-row x 128 B block per wave instruction)
-//     in stages of 64 k, two buffers: stage t+1 is in flight while stage t is multiplied. LDS rows are 128 B with
-//     the 16-byte chunks XOR-swizzled by (row / 2) mod 8, so the 16 rows one ds_read_b128 touches hit distinct banks.
+//     in stages of 64 k: an x ring of XD stages and a W ring of XD + 1, the DMAs XD stages ahead of the stage being
+//     multiplied (XD = 2 on most tiles; 4 on a 128 x 64 tile for the weight stream at M = 64). LDS rows are 128 B
+//     with the 16-byte chunks XOR-swizzled by (row / 2) mod 8, so the 16 rows one ds_read_b128 touches hit distinct
+//     banks.
 //     Half of a stage's DMA instructions go out right after the barrier that frees their buffer, the rest one per
 //     MFMA group of the following groups.
 //   * A wave walks its W fragments starting at its first extra fragment (rotated order), so the extra MFMAs sit
@@ -214,12 +216,13 @@ __device__ __forceinline__ void kx_body(const GemmParams& p) {
   if constexpr (XE > 0) xoff[FX] = (uint32_t)(xe * 16 * RB) + ro;
 
   // ------------------------------------------------------------------ LDS rings and DMA pattern
-  // LDS: a ring of WD = 3 stages of W (BN rows x 128 B = 64 k) and a ring of 2 stages of x (BM rows), 16-byte chunks
-  // XOR-swizzled by (row / 2) mod 8 within each region. A wave reads its x fragments of a stage into registers right
-  // after the barrier that publishes the stage and keeps them for the whole stage, so a second barrier a few MFMA
-  // groups later frees that x buffer: the DMAs issued then (batch t, issued as stage t begins) fetch x and W of
-  // stage t+2. Both operands get two stages to arrive; the weights come from HBM, x (the same rows for every
-  // workgroup) mostly from L2, and a wave's DMAs complete in issue order, so the x and W traffic share one queue.
+  // LDS: a ring of WD = XD + 1 stages of W (BN rows x 128 B = 64 k) and a ring of XD stages of x (BM rows), 16-byte
+  // chunks XOR-swizzled by (row / 2) mod 8 within each region. A wave reads its x fragments of a stage into
+  // registers right after the barrier that publishes the stage and keeps them for the whole stage, so a second
+  // barrier a few MFMA groups later frees that x buffer: the DMAs issued then (batch t, issued as stage t begins)
+  // fetch x and W of stage t+XD. Both operands get XD stages to arrive; the weights come from HBM, x (the same rows
+  // for every workgroup) mostly from L2, and a wave's DMAs complete in issue order, so the x and W traffic share one
+  // queue.
   constexpr int WST = BN * RB, XST = BM * RB;
   uint8_t* const wring = smem;
   uint8_t* const xring = smem + S::WD * WST;
